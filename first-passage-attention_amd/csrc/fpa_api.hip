@@ -1,0 +1,185 @@
+// fpa_api.hip -- the extern "C" entry points of libfpa.so (declared in include/fpa.h).
+//
+// Validation mirrors first_passage_attention (kernel.py:467-486 of
+// yliu-fort/first-passage-attention); scratch sizing replaces the torch allocations of
+// kernel.py:390-392, 406-407 and 430-436 so that the caller owns every buffer.
+#include <stdint.h>
+
+#include <string>
+
+#include "fpa.h"
+#include "fpa_common.h"
+#include "fpa_params.h"
+
+using namespace fpa;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string &msg) {
+    g_err = msg;
+    return code;
+}
+
+int64_t tp_of(int64_t T) { return ((T + G - 1) / G) * G; }
+int64_t align64(int64_t n) { return (n + 63) / 64 * 64; }  // floats -> 256-byte multiple
+
+struct WsLayout {
+    int64_t delta, wsum, rsum, gd, tbuf, dbp, total;  // float offsets
+};
+
+WsLayout ws_layout(int64_t B, int64_t H, int64_t T) {
+    const int64_t BH = B * H, TP = tp_of(T), NB = TP / G, NKV = (T + 127) / 128;
+    WsLayout w;
+    int64_t off = 0;
+    w.delta = off; off += align64(BH * TP);
+    w.wsum = off;  off += align64(BH * TP);
+    w.rsum = off;  off += align64(BH * TP);
+    w.gd = off;    off += align64(BH * NB * G * G);
+    w.tbuf = off;  off += align64(BH * NB * NB * 2);
+    w.dbp = off;   off += align64(BH * NKV * 4);
+    w.total = off;
+    return w;
+}
+
+S3 s3(const int64_t *s) { return S3{s[0], s[1], s[2]}; }
+
+// Shared checks of the forward and backward arguments.
+int check_common(int64_t B, int64_t H, int64_t T, int64_t D, int32_t dtype, float tau) {
+    if (B < 1 || H < 1 || T < 1) return fail(FPA_ERR_INVALID, "q, k and v must have the same shape (B, H, T, D)");
+    if (dtype != FPA_F16 && dtype != FPA_F32) return fail(FPA_ERR_INVALID, "q, k and v must all be fp16 or all fp32");
+    if (D < 16 || (D & (D - 1)) != 0)
+        return fail(FPA_ERR_INVALID, "the head dimension and the block must be powers of two >= 16");
+    if (!(tau > 0.f)) return fail(FPA_ERR_INVALID, "tau must be positive");
+    if (!supported_d(dtype, (int)D))
+        return fail(FPA_ERR_UNSUPPORTED, "head dimension " + std::to_string(D) + " is not built (16, 32, 64, 128)");
+    if (B * H > 65535) return fail(FPA_ERR_UNSUPPORTED, "B * H must be at most 65535");
+    if (tp_of(T) / G > 2048) return fail(FPA_ERR_UNSUPPORTED, "T must be at most 131072");
+    return FPA_OK;
+}
+
+// 16-byte row alignment of a (B, H, T, D) tensor with unit d stride.
+int check_rows(const void *ptr, const int64_t *st, int32_t dtype, const char *name) {
+    if (ptr == nullptr) return fail(FPA_ERR_INVALID, std::string(name) + " is NULL");
+    const int64_t ce = (dtype == FPA_F16) ? 8 : 4;
+    if ((reinterpret_cast<uintptr_t>(ptr) & 15) != 0 || st[0] % ce || st[1] % ce || st[2] % ce)
+        return fail(FPA_ERR_INVALID, std::string(name) +
+                                         " rows must be 16-byte aligned (contiguous head dimension, aligned strides)");
+    return FPA_OK;
+}
+
+int hip_fail(hipError_t e, const char *where) {
+    return fail(FPA_ERR_HIP, std::string(where) + ": " + hipGetErrorString(e));
+}
+
+}  // namespace
+
+extern "C" {
+
+int fpa_abi_version(void) { return 2; }
+
+const char *fpa_last_error(void) { return g_err.c_str(); }
+
+int64_t fpa_state_floats(int64_t B, int64_t H, int64_t T) {
+    const int64_t TP = tp_of(T);
+    return StateLayout{B * H, TP, TP / G}.total();
+}
+
+int64_t fpa_lse_floats(int64_t B, int64_t H, int64_t T) { return B * H * tp_of(T); }
+
+int64_t fpa_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D, int32_t dtype) {
+    (void)D;
+    (void)dtype;
+    return ws_layout(B, H, T).total * (int64_t)sizeof(float);
+}
+
+int fpa_fwd(const FpaFwdArgs *a, void *stream) {
+    g_err.clear();
+    if (a == nullptr) return fail(FPA_ERR_INVALID, "args is NULL");
+    int rc = check_common(a->B, a->H, a->T, a->D, a->dtype, a->tau);
+    if (rc) return rc;
+    if ((rc = check_rows(a->q, a->sq, a->dtype, "q")) || (rc = check_rows(a->k, a->sk, a->dtype, "k")) ||
+        (rc = check_rows(a->v, a->sv, a->dtype, "v")) || (rc = check_rows(a->o, a->so, a->dtype, "o")))
+        return rc;
+    if (a->sq[3] != 1 || a->sk[3] != 1 || a->sv[3] != 1 || a->so[3] != 1)
+        return fail(FPA_ERR_INVALID, "the head dimension of q, k, v and o must be contiguous");
+    if (!a->phi || !a->psi || !a->beta || !a->lse || !a->state)
+        return fail(FPA_ERR_INVALID, "phi, psi, beta, lse and state must be non-NULL");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int64_t TP = tp_of(a->T);
+    StatsParams sp;
+    sp.phi = a->phi; sp.sphi = s3(a->sphi);
+    sp.psi = a->psi; sp.spsi = s3(a->spsi);
+    sp.state = a->state;
+    sp.H = (int)a->H; sp.T = (int)a->T; sp.TP = (int)TP; sp.NB = (int)(TP / G); sp.BH = (int)(a->B * a->H);
+    sp.il2 = LOG2E / a->tau;
+    const int ph = a->phases ? a->phases : (FPA_FWD_STATS | FPA_FWD_MAIN);
+    hipError_t e;
+    if ((ph & FPA_FWD_STATS) && (e = launch_stats(sp, s)) != hipSuccess) return hip_fail(e, "fpa_stats launch");
+    FwdParams fp;
+    fp.q = a->q; fp.sq = s3(a->sq);
+    fp.k = a->k; fp.sk = s3(a->sk);
+    fp.v = a->v; fp.sv = s3(a->sv);
+    fp.o = a->o; fp.so = s3(a->so);
+    fp.beta = a->beta; fp.lse = a->lse; fp.state = a->state;
+    fp.H = sp.H; fp.T = sp.T; fp.TP = sp.TP; fp.NB = sp.NB; fp.BH = sp.BH;
+    fp.sc2 = LOG2E / sqrtf((float)a->D);
+    if ((ph & FPA_FWD_MAIN) && (e = launch_fwd(fp, a->dtype, (int)a->D, s)) != hipSuccess)
+        return hip_fail(e, "fpa_fwd launch");
+    return FPA_OK;
+}
+
+int fpa_bwd(const FpaBwdArgs *a, void *stream) {
+    g_err.clear();
+    if (a == nullptr) return fail(FPA_ERR_INVALID, "args is NULL");
+    int rc = check_common(a->B, a->H, a->T, a->D, a->dtype, a->tau);
+    if (rc) return rc;
+    if ((rc = check_rows(a->q, a->sq, a->dtype, "q")) || (rc = check_rows(a->k, a->sk, a->dtype, "k")) ||
+        (rc = check_rows(a->v, a->sv, a->dtype, "v")) || (rc = check_rows(a->o, a->so, a->dtype, "o")) ||
+        (rc = check_rows(a->dout, a->sdo, a->dtype, "do")) || (rc = check_rows(a->dq, a->sdq, a->dtype, "dq")) ||
+        (rc = check_rows(a->dk, a->sdk, a->dtype, "dk")) || (rc = check_rows(a->dv, a->sdv, a->dtype, "dv")))
+        return rc;
+    if (a->sq[3] != 1 || a->sk[3] != 1 || a->sv[3] != 1 || a->so[3] != 1 || a->sdo[3] != 1 || a->sdq[3] != 1 ||
+        a->sdk[3] != 1 || a->sdv[3] != 1)
+        return fail(FPA_ERR_INVALID, "the head dimension of every (B, H, T, D) tensor must be contiguous");
+    if (!a->beta || !a->lse || !a->state || !a->dphi || !a->dpsi || !a->dbeta || !a->workspace)
+        return fail(FPA_ERR_INVALID, "beta, lse, state, dphi, dpsi, dbeta and workspace must be non-NULL");
+    if ((reinterpret_cast<uintptr_t>(a->workspace) & 255) != 0)
+        return fail(FPA_ERR_INVALID, "workspace must be 256-byte aligned");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int64_t TP = tp_of(a->T);
+    const WsLayout wl = ws_layout(a->B, a->H, a->T);
+    float *ws = static_cast<float *>(a->workspace);
+    BwdParams p;
+    p.q = a->q; p.sq = s3(a->sq);
+    p.k = a->k; p.sk = s3(a->sk);
+    p.v = a->v; p.sv = s3(a->sv);
+    p.o = a->o; p.so = s3(a->so);
+    p.dout = a->dout; p.sdo = s3(a->sdo);
+    p.dq = a->dq; p.sdq = s3(a->sdq);
+    p.dk = a->dk; p.sdk = s3(a->sdk);
+    p.dv = a->dv; p.sdv = s3(a->sdv);
+    p.beta = a->beta; p.lse = a->lse; p.state = a->state;
+    p.dphi = a->dphi; p.dpsi = a->dpsi; p.dbeta = a->dbeta;
+    p.delta = ws + wl.delta; p.wsum = ws + wl.wsum; p.rsum = ws + wl.rsum;
+    p.gd = ws + wl.gd; p.tbuf = ws + wl.tbuf; p.dbp = ws + wl.dbp;
+    p.B = (int)a->B; p.H = (int)a->H; p.T = (int)a->T; p.TP = (int)TP; p.NB = (int)(TP / G);
+    p.BH = (int)(a->B * a->H); p.NKV = (int)((a->T + 127) / 128);
+    p.sc2 = LOG2E / sqrtf((float)a->D);
+    p.smscale = 1.0f / sqrtf((float)a->D);
+    p.il2 = LOG2E / a->tau;
+    const int ph = a->phases ? a->phases : 31;
+    hipError_t e;
+    if ((ph & FPA_BWD_DELTA) && (e = launch_bwd_prep(p, a->dtype, (int)a->D, s)) != hipSuccess)
+        return hip_fail(e, "fpa_bwd_prep launch");
+    if ((ph & FPA_BWD_KEYS) && (e = launch_bwd_kv(p, a->dtype, (int)a->D, s)) != hipSuccess)
+        return hip_fail(e, "fpa_bwd_kv launch");
+    if ((ph & FPA_BWD_QUERIES) && (e = launch_bwd_q(p, a->dtype, (int)a->D, s)) != hipSuccess)
+        return hip_fail(e, "fpa_bwd_q launch");
+    if ((ph & FPA_BWD_PHI) && (e = launch_bwd_combine(p, s)) != hipSuccess) return hip_fail(e, "fpa_bwd_combine launch");
+    if ((ph & FPA_BWD_BETA) && (e = launch_bwd_dbeta(p, s)) != hipSuccess) return hip_fail(e, "fpa_bwd_dbeta launch");
+    return FPA_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,302 @@
+// fpa_common.h -- shared device code for the gfx950 First Passage Attention kernels.
+//
+// Conventions used by every kernel in this directory.
+//
+// * One head = one (b, h) pair, flattened to bh = b * H + h.  Positions are cut
+//   into blocks of G = 64; TP = T rounded up to G, NB = TP / G.
+// * Logits are kept in base 2: logit2 = (q.k / sqrt(D) + bias) * log2(e), so the
+//   softmax uses exp2 and the saved row statistic lse2 is a base-2 log-sum-exp.
+// * Matrix products run on the 32x32 MFMA of gfx950:
+//     fp16: v_mfma_f32_32x32x16_f16  (one K step contracts 16 indices)
+//     fp32: v_mfma_f32_32x32x2_f32   (one K step contracts 2 indices)
+//   Lane l = 32 * g + c (g = l / 32, c = l % 32).  A operand: lane holds row c;
+//   B operand: lane holds column c; lane group g holds its half of the K step.
+//   The 32x32 accumulator: register j of lane l is C[8*(j/4) + 4*g + j%4][c].
+// * A contraction index may be permuted freely as long as both operands use the
+//   same permutation.  Three operand access patterns are used:
+//     P1  row-major source X[row][k], k contiguous (LDS or registers):
+//         fp16 step ks: X[row][16*ks + 8*g .. +8];
+//         fp32 step st: X[row][g*K/2 + st].
+//     P2  the accumulator of a previous product, its rows becoming the K index:
+//         fp16 step ks of tile mt = ks/2: registers 8*(ks%2) .. +8, i.e. rows
+//              32*mt + 16*(ks%2) + 8*(e/4) + 4*g + e%4 for element e;
+//         fp32 step (mt, j): register j, i.e. row 32*mt + 8*(j/4) + 4*g + j%4.
+//     P3  the partner of P2, read from a transposed source XT[n][krow]:
+//         fp16: XT[n][R .. R+3] and XT[n][R+8 .. R+11], R = 32*mt + 16*(ks%2) + 4*g;
+//         fp32: XT[n][32*mt + 8*(j/4) + 4*g + j%4] (4 steps per 16-byte read).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fpa {
+
+typedef _Float16 f16;
+typedef f16 h8 __attribute__((ext_vector_type(8)));
+typedef f16 h4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr int G = 64;        // statistics block
+constexpr int NTHREADS = 256;
+
+__device__ __forceinline__ float pinf() { return __builtin_inff(); }
+__device__ __forceinline__ float ninf() { return -__builtin_inff(); }
+__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float frcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float flog2(float x) { return __builtin_amdgcn_logf(x); }
+
+// log2(2^a + 2^b) with -inf handled (both -inf -> -inf).
+__device__ __forceinline__ float lse2_pair(float a, float b) {
+    float m = fmaxf(a, b);
+    if (m == ninf()) return m;
+    float d = fminf(a, b) - m;
+    return m + flog2(1.0f + fexp2(d));
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+    f32x16 z;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) z[i] = 0.f;
+    return z;
+}
+
+// ---------------------------------------------------------------------------
+// MFMA traits
+// ---------------------------------------------------------------------------
+template <typename T> struct MT;
+
+template <> struct MT<f16> {
+    typedef h8 op_t;
+    static constexpr int KSTEP = 16;
+    static constexpr int CHUNK = 8;  // elements per 16-byte global/LDS chunk
+    __device__ static __forceinline__ f32x16 mma(op_t a, op_t b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <> struct MT<float> {
+    typedef float op_t;
+    static constexpr int KSTEP = 2;
+    static constexpr int CHUNK = 4;
+    __device__ static __forceinline__ f32x16 mma(op_t a, op_t b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+    }
+};
+
+// Number of P1 operands that cover a contraction of length K (K = D here).
+template <typename T, int K> struct P1Count {
+    static constexpr int N = (sizeof(T) == 2) ? K / 16 : K / 2;
+};
+// Register array of the P1 operands of one row.
+template <typename T, int K> using OpRow = typename MT<T>::op_t[P1Count<T, K>::N];
+
+// P1 operand `i` for contraction length K from a row-major source row (LDS or global).
+template <typename T, int K>
+__device__ __forceinline__ typename MT<T>::op_t p1_load(const T *row, int g, int i);
+
+template <>
+__device__ __forceinline__ h8 p1_load<f16, 16>(const f16 *row, int g, int i) {
+    return *reinterpret_cast<const h8 *>(row + 16 * i + 8 * g);
+}
+#define FPA_P1_F16(K)                                                                 \
+    template <>                                                                       \
+    __device__ __forceinline__ h8 p1_load<f16, K>(const f16 *row, int g, int i) {     \
+        return *reinterpret_cast<const h8 *>(row + 16 * i + 8 * g);                   \
+    }
+FPA_P1_F16(32)
+FPA_P1_F16(64)
+FPA_P1_F16(128)
+FPA_P1_F16(256)
+#undef FPA_P1_F16
+#define FPA_P1_F32(K)                                                                 \
+    template <>                                                                       \
+    __device__ __forceinline__ float p1_load<float, K>(const float *row, int g, int i) { \
+        return row[g * (K / 2) + i];                                                  \
+    }
+FPA_P1_F32(16)
+FPA_P1_F32(32)
+FPA_P1_F32(64)
+FPA_P1_F32(128)
+FPA_P1_F32(256)
+#undef FPA_P1_F32
+
+// All P1 operands of one row, read with 16-byte loads (row must be 16-byte aligned).
+template <typename T, int K>
+__device__ __forceinline__ void p1_load_row(OpRow<T, K> &dst, const T *row, int g) {
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+        for (int i = 0; i < K / 16; ++i) dst[i] = *reinterpret_cast<const h8 *>(row + 16 * i + 8 * g);
+    } else {
+#pragma unroll
+        for (int i = 0; i < K / 8; ++i) {
+            f32x4 v = *reinterpret_cast<const f32x4 *>(row + g * (K / 2) + 4 * i);
+            dst[4 * i + 0] = v[0];
+            dst[4 * i + 1] = v[1];
+            dst[4 * i + 2] = v[2];
+            dst[4 * i + 3] = v[3];
+        }
+    }
+}
+
+template <typename T, int K>
+__device__ __forceinline__ void p1_zero(OpRow<T, K> &dst) {
+#pragma unroll
+    for (int i = 0; i < P1Count<T, K>::N; ++i) {
+        if constexpr (sizeof(T) == 2) {
+            h8 z;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) z[e] = (f16)0.f;
+            dst[i] = z;
+        } else {
+            dst[i] = 0.f;
+        }
+    }
+}
+
+// acc += A * B over a contraction of length K, both operands P1 (A from an LDS row, B in registers).
+template <typename T, int K>
+__device__ __forceinline__ f32x16 mma_p1_lds_reg(f32x16 acc, const T *arow, int g, const OpRow<T, K> &breg) {
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+        for (int i = 0; i < K / 16; ++i)
+            acc = MT<T>::mma(*reinterpret_cast<const h8 *>(arow + 16 * i + 8 * g), breg[i], acc);
+    } else {
+#pragma unroll
+        for (int i = 0; i < K / 8; ++i) {
+            f32x4 a = *reinterpret_cast<const f32x4 *>(arow + g * (K / 2) + 4 * i);
+            acc = MT<T>::mma(a[0], breg[4 * i + 0], acc);
+            acc = MT<T>::mma(a[1], breg[4 * i + 1], acc);
+            acc = MT<T>::mma(a[2], breg[4 * i + 2], acc);
+            acc = MT<T>::mma(a[3], breg[4 * i + 3], acc);
+        }
+    }
+    return acc;
+}
+
+// acc += A * B where A (or B) comes from accumulator tiles c[0..NT) (P2) and the partner from
+// the transposed LDS row xt[krow] (P3).  `a_is_p3` selects which operand slot the P3 value takes:
+// true -> P3 is the A operand (rows of the product indexed by the transposed source's n);
+// false -> P3 is the B operand.
+template <typename T, int NT, bool A_IS_P3>
+__device__ __forceinline__ f32x16 mma_p2_p3(f32x16 acc, const f32x16 (&c)[NT], const T *xt, int g) {
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+        for (int mt = 0; mt < NT; ++mt) {
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                h8 p2;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) p2[e] = (f16)c[mt][8 * hf + e];
+                const int R = 32 * mt + 16 * hf + 4 * g;
+                h4 lo = *reinterpret_cast<const h4 *>(xt + R);
+                h4 hi = *reinterpret_cast<const h4 *>(xt + R + 8);
+                h8 p3 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                acc = A_IS_P3 ? MT<T>::mma(p3, p2, acc) : MT<T>::mma(p2, p3, acc);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int mt = 0; mt < NT; ++mt) {
+#pragma unroll
+            for (int jq = 0; jq < 4; ++jq) {
+                f32x4 p3 = *reinterpret_cast<const f32x4 *>(xt + 32 * mt + 8 * jq + 4 * g);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float p2 = c[mt][4 * jq + e];
+                    acc = A_IS_P3 ? MT<T>::mma(p3[e], p2, acc) : MT<T>::mma(p2, p3[e], acc);
+                }
+            }
+        }
+    }
+    return acc;
+}
+
+// ---------------------------------------------------------------------------
+// Global -> LDS staging.  Rows r in [0, NR) of a (B, H, T, D)-strided tensor at
+// positions row0 + r; rows at or past T are zero-filled.
+// ---------------------------------------------------------------------------
+template <typename T, int D, int NR, int PITCH>
+__device__ __forceinline__ void stage_rows(T *dst, const T *src, int64_t st, int row0, int T_) {
+    constexpr int CE = MT<T>::CHUNK;
+    constexpr int CPR = (D + CE - 1) / CE;    // chunks per row
+    for (int idx = threadIdx.x; idx < NR * CPR; idx += NTHREADS) {
+        const int r = idx / CPR, cc = idx % CPR;
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        if (row0 + r < T_) v = *reinterpret_cast<const f32x4 *>(src + (int64_t)(row0 + r) * st + cc * CE);
+        *reinterpret_cast<f32x4 *>(dst + r * PITCH + cc * CE) = v;
+    }
+}
+
+// Transposed staging: dst[d][r] = src[row0 + r][d] for d < D, r < NR (rows >= T -> 0).
+template <typename T, int D, int NR, int PITCHT>
+__device__ __forceinline__ void stage_rows_t(T *dst, const T *src, int64_t st, int row0, int T_) {
+    constexpr int CE = MT<T>::CHUNK;
+    constexpr int CPR = (D + CE - 1) / CE;
+    constexpr int UNITS = (NR / 4) * CPR;     // 4 rows x one chunk per unit
+    for (int idx = threadIdx.x; idx < UNITS; idx += NTHREADS) {
+        const int r4 = idx / CPR, cc = idx % CPR;
+        const int r = 4 * r4;
+        if constexpr (sizeof(T) == 2) {
+            h8 v[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (row0 + r + i < T_)
+                    v[i] = *reinterpret_cast<const h8 *>(src + (int64_t)(row0 + r + i) * st + cc * CE);
+                else
+                    v[i] = h8{0, 0, 0, 0, 0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int e = 0; e < CE; ++e) {
+                h4 w = {v[0][e], v[1][e], v[2][e], v[3][e]};
+                *reinterpret_cast<h4 *>(dst + (cc * CE + e) * PITCHT + r) = w;
+            }
+        } else {
+            f32x4 v[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (row0 + r + i < T_)
+                    v[i] = *reinterpret_cast<const f32x4 *>(src + (int64_t)(row0 + r + i) * st + cc * CE);
+                else
+                    v[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int e = 0; e < CE; ++e) {
+                f32x4 w = {v[0][e], v[1][e], v[2][e], v[3][e]};
+                *reinterpret_cast<f32x4 *>(dst + (cc * CE + e) * PITCHT + r) = w;
+            }
+        }
+    }
+}
+
+// Register P1 operands of one global row (zeros when the row is past T).
+template <typename T, int D>
+__device__ __forceinline__ void load_row_p1(OpRow<T, D> &dst, const T *rowp, bool valid, int g) {
+    if (valid)
+        p1_load_row<T, D>(dst, rowp, g);
+    else
+        p1_zero<T, D>(dst);
+}
+
+// Sum over the 64 lanes of a wave, fixed order (butterfly).
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o, 64);
+    return x;
+}
+
+// Element (row, column) of accumulator register j for lane group g (column = lane % 32).
+__device__ __forceinline__ constexpr int acc_row(int j, int g) { return 8 * (j / 4) + 4 * g + (j % 4); }
+
+// State planes (float offsets), each plane is BH * TP floats except the two block planes.
+struct StateLayout {
+    int64_t BH, TP, NB;
+    __host__ __device__ int64_t plane(int k) const { return (int64_t)k * BH * TP; }  // 0..5
+    __host__ __device__ int64_t bplane(int k) const { return 6 * BH * TP + (int64_t)k * BH * NB; }  // 0..1
+    __host__ __device__ int64_t total() const { return 6 * BH * TP + 2 * BH * NB; }
+};
+enum { PL_PHI = 0, PL_PSI = 1, PL_PRE = 2, PL_PREL = 3, PL_SUF = 4, PL_SUFL = 5 };
+enum { BP_MIN = 0, BP_LSE = 1 };
+
+}  // namespace fpa

@@ -1,0 +1,271 @@
+// fpa_fwd.hip -- block statistics and the forward pass of First Passage Attention.
+//
+// Reference behaviour: kernel.py:83-100 (_stats) and kernel.py:103-162 (_fwd) of
+// yliu-fort/first-passage-attention.  Same maths, gfx950 design:
+//   * statistics: one wave per block of G = 64 positions, prefix/suffix min and
+//     base-2 log-sum-exp by wave shuffles;
+//   * forward: a workgroup of 4 waves owns 128 query rows (32 per wave), streams
+//     64-key tiles from the diagonal down to key 0 through LDS (K row-major, V
+//     transposed), computes S^T = K Q^T and O^T += V^T P^T on the 32x32 MFMA, and
+//     keeps each query's online-softmax state in its own lane.
+#include "fpa_common.h"
+#include "fpa_params.h"
+
+namespace fpa {
+
+// ---------------------------------------------------------------------------
+// Block statistics (per head, per 64-block):
+//   PHI, PSI  : contiguous float copies (phi = +inf past T)
+//   PRE_t     = min phi[sb .. t]           PREL_t = log2 sum 2^a[sb .. t]
+//   SUF_s     = min phi(s .. eb)           SUFL_s = log2 sum 2^a(s .. eb)
+//   BMIN, BLSE: the whole block.           a_u = -phi_u * log2(e) / tau
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(64) fpa_stats_kernel(StatsParams p) {
+    const int blk = blockIdx.x, bh = blockIdx.y;
+    const int b = bh / p.H, h = bh % p.H;
+    const int lane = threadIdx.x;
+    const int u = blk * G + lane;
+    float ph = pinf(), ps = 0.f;
+    if (u < p.T) {
+        ph = p.phi[b * p.sphi.b + h * p.sphi.h + (int64_t)u * p.sphi.t];
+        ps = p.psi[b * p.spsi.b + h * p.spsi.h + (int64_t)u * p.spsi.t];
+    }
+    const float a = (u < p.T) ? -ph * p.il2 : ninf();
+
+    float pm = ph, pl = a;  // inclusive prefix
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float ym = __shfl_up(pm, o, 64);
+        const float yl = __shfl_up(pl, o, 64);
+        if (lane >= o) {
+            pm = fminf(pm, ym);
+            pl = lse2_pair(pl, yl);
+        }
+    }
+    float sm = ph, sl = a;  // inclusive suffix
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float ym = __shfl_down(sm, o, 64);
+        const float yl = __shfl_down(sl, o, 64);
+        if (lane + o < 64) {
+            sm = fminf(sm, ym);
+            sl = lse2_pair(sl, yl);
+        }
+    }
+    float suf = __shfl_down(sm, 1, 64), sufl = __shfl_down(sl, 1, 64);  // strictly after
+    if (lane == 63) {
+        suf = pinf();
+        sufl = ninf();
+    }
+    StateLayout L{p.BH, p.TP, p.NB};
+    const int64_t r = (int64_t)bh * p.TP + u;
+    p.state[L.plane(PL_PHI) + r] = ph;
+    p.state[L.plane(PL_PSI) + r] = ps;
+    p.state[L.plane(PL_PRE) + r] = pm;
+    p.state[L.plane(PL_PREL) + r] = pl;
+    p.state[L.plane(PL_SUF) + r] = suf;
+    p.state[L.plane(PL_SUFL) + r] = sufl;
+    if (lane == 63) {
+        p.state[L.bplane(BP_MIN) + (int64_t)bh * p.NB + blk] = pm;
+        p.state[L.bplane(BP_LSE) + (int64_t)bh * p.NB + blk] = pl;
+    }
+}
+
+hipError_t launch_stats(const StatsParams &p, hipStream_t s) {
+    hipLaunchKernelGGL(fpa_stats_kernel, dim3(p.NB, p.BH), dim3(64), 0, s, p);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Forward.
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__global__ void __launch_bounds__(NTHREADS) fpa_fwd_kernel(FwdParams p) {
+    constexpr int BM = 128, BN = 64;
+    constexpr int DT = D < 32 ? 32 : D;
+    constexpr int NDT = DT / 32;
+    constexpr int PK = D + (sizeof(T) == 2 ? 8 : 4);  // K tile pitch (elements)
+    constexpr int PV = BN + 4;                          // V^T tile pitch (elements)
+    __shared__ __attribute__((aligned(16))) T Ks[BN * PK];
+    __shared__ __attribute__((aligned(16))) T VT[DT * PV];
+    __shared__ float sSUF[BN], sPSI[BN], sPHI[BN];
+
+    const int tid = threadIdx.x, w = tid / 64, lane = tid % 64, g = lane / 32, c = lane % 32;
+    const int qt = gridDim.x - 1 - blockIdx.x;  // longest rows first
+    const int bh = blockIdx.y, b = bh / p.H, h = bh % p.H;
+    const int q0 = qt * BM, qw0 = q0 + 32 * w, tq = qw0 + c;
+    const int ib = qw0 / G;
+    const bool wave_active = qw0 < p.T;
+    const StateLayout L{p.BH, p.TP, p.NB};
+    const int64_t rowbase = (int64_t)bh * p.TP;
+
+    const T *Qb = static_cast<const T *>(p.q) + b * p.sq.b + h * p.sq.h;
+    const T *Kb = static_cast<const T *>(p.k) + b * p.sk.b + h * p.sk.h;
+    const T *Vb = static_cast<const T *>(p.v) + b * p.sv.b + h * p.sv.h;
+
+    OpRow<T, D> qreg;
+    load_row_p1<T, D>(qreg, Qb + (int64_t)tq * p.sq.t, tq < p.T, g);
+
+    const float betal = p.beta[h] * LOG2E;
+    const float pre_t = (tq < p.TP) ? p.state[L.plane(PL_PRE) + rowbase + tq] : pinf();
+
+    if constexpr (D < DT) {  // rows D..31 of V^T stay zero
+        for (int i = tid; i < (DT - D) * PV; i += NTHREADS) VT[D * PV + i] = (T)0.f;
+    }
+
+    float m_i = ninf(), l_i = 0.f;
+    f32x16 oacc[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) oacc[dt] = zero16();
+
+    const int nkt = (p.T + BN - 1) / BN;
+    const int jtmax = min(nkt - 1, (q0 + BM - 1) / BN);
+    float mid = pinf();  // min phi over the blocks strictly between the key block and ib
+
+    for (int jt = jtmax; jt >= 0; --jt) {
+        const int s0 = jt * BN;
+        __syncthreads();
+        stage_rows<T, D, BN, PK>(Ks, Kb, p.sk.t, s0, p.T);
+        stage_rows_t<T, D, BN, PV>(VT, Vb, p.sv.t, s0, p.T);
+        if (tid < BN) {
+            sSUF[tid] = p.state[L.plane(PL_SUF) + rowbase + s0 + tid];
+            sPSI[tid] = p.state[L.plane(PL_PSI) + rowbase + s0 + tid];
+            sPHI[tid] = p.state[L.plane(PL_PHI) + rowbase + s0 + tid];
+        }
+        __syncthreads();
+        if (!wave_active || s0 > qw0 + 31) continue;
+
+        f32x16 s[2];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) s[mt] = mma_p1_lds_reg<T, D>(zero16(), Ks + (32 * mt + c) * PK, g, qreg);
+
+        const int jb = jt;  // BN == G: the key tile is one statistics block
+        if (jb < ib) {
+            const float Y = fminf(pre_t, mid);
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const int sr = 32 * mt + acc_row(j, g);
+                    const float x = fminf(sSUF[sr], Y) - sPSI[sr];
+                    s[mt][j] = s[mt][j] * p.sc2 + betal * fminf(x, 0.f);
+                }
+        } else {
+            // Diagonal block: X_ts = min phi(s, t] inside the block, by a descending scan.
+            const int tr = tq - s0;
+            float X[2][16];
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) X[mt][j] = pinf();
+            float r = pinf();
+#pragma unroll
+            for (int u = BN - 1; u >= 1; --u) {
+                const float ph = sPHI[u];
+                r = (u <= tr) ? fminf(r, ph) : r;
+                const int sr = u - 1, mt = sr >> 5, jj = sr & 31;
+                const int gg = (jj >> 2) & 1, j = (jj >> 3) * 4 + (jj & 3);
+                if (gg == g) X[mt][j] = r;
+            }
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const int sr = 32 * mt + acc_row(j, g);
+                    float z;
+                    if (sr > tr || s0 + sr >= p.T)
+                        z = ninf();
+                    else if (sr == tr)
+                        z = s[mt][j] * p.sc2;
+                    else
+                        z = s[mt][j] * p.sc2 + betal * fminf(X[mt][j] - sPSI[sr], 0.f);
+                    s[mt][j] = z;
+                }
+        }
+
+        // Online softmax (base 2).  Lanes c and c+32 hold the same query.
+        float mx = ninf();
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[mt][j]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m_i, mx);
+        const float m_use = (m_new == ninf()) ? 0.f : m_new;
+        const float alpha = fexp2(m_i - m_use);
+        float rs = 0.f;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const float pv = fexp2(s[mt][j] - m_use);
+                s[mt][j] = pv;
+                rs += pv;
+            }
+        rs += __shfl_xor(rs, 32, 64);
+        l_i = l_i * alpha + rs;
+        m_i = m_new;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) oacc[dt][j] *= alpha;
+
+        // O^T[d][t] += V^T[d][s] P^T[s][t]
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mma_p2_p3<T, 2, true>(oacc[dt], s, VT + (32 * dt + c) * PV, g);
+
+        if (jb < ib) mid = fminf(mid, p.state[L.bplane(BP_MIN) + (int64_t)bh * p.NB + jb]);
+    }
+
+    if (!wave_active) return;
+    const float inv = 1.f / l_i;
+    if (tq < p.T) {
+        T *Orow = static_cast<T *>(p.o) + b * p.so.b + h * p.so.h + (int64_t)tq * p.so.t;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int jq = 0; jq < 4; ++jq) {
+                const int d0 = 32 * dt + 8 * jq + 4 * g;
+                if (d0 < D) {
+                    if constexpr (sizeof(T) == 2) {
+                        h4 v4 = {(f16)(oacc[dt][4 * jq + 0] * inv), (f16)(oacc[dt][4 * jq + 1] * inv),
+                                 (f16)(oacc[dt][4 * jq + 2] * inv), (f16)(oacc[dt][4 * jq + 3] * inv)};
+                        *reinterpret_cast<h4 *>(Orow + d0) = v4;
+                    } else {
+                        f32x4 v4 = {oacc[dt][4 * jq + 0] * inv, oacc[dt][4 * jq + 1] * inv,
+                                    oacc[dt][4 * jq + 2] * inv, oacc[dt][4 * jq + 3] * inv};
+                        *reinterpret_cast<f32x4 *>(Orow + d0) = v4;
+                    }
+                }
+            }
+    }
+    if (g == 0 && tq < p.TP) p.lse[rowbase + tq] = m_i + flog2(l_i);
+}
+
+template <typename T, int D>
+static hipError_t launch_fwd_t(const FwdParams &p, hipStream_t s) {
+    const int nqt = (p.T + 127) / 128;
+    hipLaunchKernelGGL((fpa_fwd_kernel<T, D>), dim3(nqt, p.BH), dim3(NTHREADS), 0, s, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_fwd(const FwdParams &p, int dtype, int D, hipStream_t s) {
+    if (dtype == 0) {
+        switch (D) {
+            case 16: return launch_fwd_t<f16, 16>(p, s);
+            case 32: return launch_fwd_t<f16, 32>(p, s);
+            case 64: return launch_fwd_t<f16, 64>(p, s);
+            case 128: return launch_fwd_t<f16, 128>(p, s);
+        }
+    } else {
+        switch (D) {
+            case 16: return launch_fwd_t<float, 16>(p, s);
+            case 32: return launch_fwd_t<float, 32>(p, s);
+            case 64: return launch_fwd_t<float, 64>(p, s);
+            case 128: return launch_fwd_t<float, 128>(p, s);
+        }
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace fpa

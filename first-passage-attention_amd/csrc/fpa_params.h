@@ -1,0 +1,77 @@
+// fpa_params.h -- kernel parameter blocks and launcher entry points (host <-> device).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fpa {
+
+// Element strides (b, h, t) of a (B, H, T, D) tensor whose d stride is 1.
+struct S3 {
+    int64_t b, h, t;
+};
+
+struct StatsParams {
+    const float *phi; S3 sphi;
+    const float *psi; S3 spsi;
+    float *state;
+    int H, T, TP, NB, BH;
+    float il2;  // log2(e) / tau
+};
+
+struct FwdParams {
+    const void *q; S3 sq;
+    const void *k; S3 sk;
+    const void *v; S3 sv;
+    void *o; S3 so;
+    const float *beta;
+    float *lse;          // BH * TP
+    const float *state;  // block statistics
+    int H, T, TP, NB, BH;
+    float sc2;           // log2(e) / sqrt(D)
+};
+
+struct BwdParams {
+    const void *q; S3 sq;
+    const void *k; S3 sk;
+    const void *v; S3 sv;
+    const void *o; S3 so;
+    const void *dout; S3 sdo;
+    void *dq; S3 sdq;
+    void *dk; S3 sdk;
+    void *dv; S3 sdv;
+    const float *beta;
+    const float *lse;
+    const float *state;
+    float *dphi;   // (B, H, T) contiguous
+    float *dpsi;   // (B, H, T) contiguous
+    float *dbeta;  // (H,)
+    // workspace regions
+    float *delta;  // BH * TP
+    float *wsum;   // BH * TP   key-block soft-min sums W_s
+    float *rsum;   // BH * TP   query-block soft-min sums R_t
+    float *gd;     // BH * NB * G * G   gated dS of in-block pairs, [s][t]
+    float *tbuf;   // BH * NB * NB * 2  middle-block sums (two 32-key halves)
+    float *dbp;    // BH * NKV * 4      dbeta partials
+    int B, H, T, TP, NB, BH, NKV;
+    float sc2;     // log2(e) / sqrt(D)
+    float smscale; // 1 / sqrt(D)
+    float il2;     // log2(e) / tau
+};
+
+// Launchers (defined next to their kernels); return hipSuccess or the launch error.
+hipError_t launch_stats(const StatsParams &p, hipStream_t s);
+hipError_t launch_fwd(const FwdParams &p, int dtype, int D, hipStream_t s);
+hipError_t launch_bwd_prep(const BwdParams &p, int dtype, int D, hipStream_t s);
+hipError_t launch_bwd_kv(const BwdParams &p, int dtype, int D, hipStream_t s);
+hipError_t launch_bwd_q(const BwdParams &p, int dtype, int D, hipStream_t s);
+hipError_t launch_bwd_combine(const BwdParams &p, hipStream_t s);
+hipError_t launch_bwd_dbeta(const BwdParams &p, hipStream_t s);
+
+// Head dimensions with built kernels.
+inline bool supported_d(int dtype, int D) {
+    (void)dtype;
+    return D == 16 || D == 32 || D == 64 || D == 128;
+}
+
+}  // namespace fpa

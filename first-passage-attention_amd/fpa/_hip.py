@@ -1,0 +1,135 @@
+"""Autograd Function that runs First Passage Attention on the gfx950 HIP kernels.
+
+Replaces the reference's ``_FirstPassageAttention`` (kernel.py:415-451): the forward
+enqueues the block statistics and the forward kernel (``fpa_fwd``), the backward
+enqueues the five backward kernels (``fpa_bwd``).  torch allocates every output
+and scratch buffer; the kernels run on torch's current stream with no host sync.
+Unlike the reference, q/k/v and do are read through their strides (no padding to a
+multiple of the block and no ``.contiguous()`` copy for the layer's permuted views);
+a tensor is copied only when its head dimension is not contiguous or its rows are
+not 16-byte aligned.
+"""
+import torch
+
+from . import _lib
+
+
+def _rows_ok(t):
+    ce = 8 if t.dtype == torch.float16 else 4
+    s = t.stride()
+    return s[3] == 1 and t.data_ptr() % 16 == 0 and all(x % ce == 0 for x in s[:3])
+
+
+def rows(t):
+    """t itself when the kernels can read it through its strides, else a contiguous copy."""
+    return t if _rows_ok(t) else t.contiguous()
+
+
+class FwdBuffers:
+    """Outputs and saved state of one forward call (all allocated by torch on q's device)."""
+
+    def __init__(self, q):
+        L = _lib.lib()
+        B, H, T, D = q.shape
+        dev = q.device
+        self.o = torch.empty((B, H, T, D), dtype=q.dtype, device=dev)
+        self.lse = torch.empty(L.fpa_lse_floats(B, H, T), dtype=torch.float32, device=dev)
+        self.state = torch.empty(L.fpa_state_floats(B, H, T), dtype=torch.float32, device=dev)
+
+
+class BwdBuffers:
+    """Gradients and scratch of one backward call."""
+
+    def __init__(self, q):
+        L = _lib.lib()
+        B, H, T, D = q.shape
+        dev = q.device
+        self.dq = torch.empty((B, H, T, D), dtype=q.dtype, device=dev)
+        self.dk = torch.empty_like(self.dq)
+        self.dv = torch.empty_like(self.dq)
+        self.dphi = torch.empty((B, H, T), dtype=torch.float32, device=dev)
+        self.dpsi = torch.empty_like(self.dphi)
+        self.dbeta = torch.empty(H, dtype=torch.float32, device=dev)
+        self.ws = torch.empty(L.fpa_bwd_workspace_bytes(B, H, T, D, _lib.dtype_code(q.dtype)),
+                              dtype=torch.uint8, device=dev)
+
+
+def fwd_args(q, k, v, phi, psi, beta, tau, out):
+    """FpaFwdArgs for fpa_fwd (q/k/v already passed through rows(); phi, psi, beta float32)."""
+    B, H, T, D = q.shape
+    a = _lib.FpaFwdArgs()
+    a.B, a.H, a.T, a.D = B, H, T, D
+    a.dtype = _lib.dtype_code(q.dtype)
+    a.tau = float(tau)
+    a.q, a.sq = _lib.ptr(q), _lib.strides4(q)
+    a.k, a.sk = _lib.ptr(k), _lib.strides4(k)
+    a.v, a.sv = _lib.ptr(v), _lib.strides4(v)
+    a.phi, a.sphi = _lib.ptr(phi), _lib.strides3(phi)
+    a.psi, a.spsi = _lib.ptr(psi), _lib.strides3(psi)
+    a.beta = _lib.ptr(beta)
+    a.o, a.so = _lib.ptr(out.o), _lib.strides4(out.o)
+    a.lse, a.state = _lib.ptr(out.lse), _lib.ptr(out.state)
+    a.phases = 0
+    return a
+
+
+def bwd_args(q, k, v, beta, tau, fwd, do, grads):
+    """FpaBwdArgs for fpa_bwd."""
+    B, H, T, D = q.shape
+    a = _lib.FpaBwdArgs()
+    a.B, a.H, a.T, a.D = B, H, T, D
+    a.dtype = _lib.dtype_code(q.dtype)
+    a.tau = float(tau)
+    a.q, a.sq = _lib.ptr(q), _lib.strides4(q)
+    a.k, a.sk = _lib.ptr(k), _lib.strides4(k)
+    a.v, a.sv = _lib.ptr(v), _lib.strides4(v)
+    a.beta = _lib.ptr(beta)
+    a.o, a.so = _lib.ptr(fwd.o), _lib.strides4(fwd.o)
+    a.dout, a.sdo = _lib.ptr(do), _lib.strides4(do)
+    a.lse, a.state = _lib.ptr(fwd.lse), _lib.ptr(fwd.state)
+    a.dq, a.sdq = _lib.ptr(grads.dq), _lib.strides4(grads.dq)
+    a.dk, a.sdk = _lib.ptr(grads.dk), _lib.strides4(grads.dk)
+    a.dv, a.sdv = _lib.ptr(grads.dv), _lib.strides4(grads.dv)
+    a.dphi, a.dpsi, a.dbeta = _lib.ptr(grads.dphi), _lib.ptr(grads.dpsi), _lib.ptr(grads.dbeta)
+    a.workspace = _lib.ptr(grads.ws)
+    a.phases = 0
+    return a
+
+
+def run_fwd(args, device):
+    _lib.check(_lib.lib().fpa_fwd(args, _lib.stream_of(device)))
+
+
+def run_bwd(args, device):
+    _lib.check(_lib.lib().fpa_bwd(args, _lib.stream_of(device)))
+
+
+class _Saved:
+    def __init__(self, o, lse, state):
+        self.o, self.lse, self.state = o, lse, state
+
+
+class FirstPassageAttentionHIP(torch.autograd.Function):
+    """o = FPA(q, k, v, phi, psi, beta); phi/psi/beta are float32, beta is (H,)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, phi, psi, beta, tau):
+        q, k, v = rows(q), rows(k), rows(v)
+        beta = beta.contiguous()
+        dev = q.device
+        with torch.cuda.device(dev):
+            out = FwdBuffers(q)
+            run_fwd(fwd_args(q, k, v, phi, psi, beta, tau, out), dev)
+        ctx.save_for_backward(q, k, v, out.o, out.lse, out.state, beta)
+        ctx.tau = float(tau)
+        return out.o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, o, lse, state, beta = ctx.saved_tensors
+        dev = q.device
+        do = rows(do.to(q.dtype))
+        with torch.cuda.device(dev):
+            grads = BwdBuffers(q)
+            run_bwd(bwd_args(q, k, v, beta, ctx.tau, _Saved(o, lse, state), do, grads), dev)
+        return grads.dq, grads.dk, grads.dv, grads.dphi, grads.dpsi, grads.dbeta, None

@@ -1,0 +1,112 @@
+"""ctypes binding of libfpa.so (the C ABI declared in include/fpa.h).
+
+The library is built in-tree by ``first-passage-attention_amd/build.py`` and lives
+next to this file.  Loading it never compiles anything; a missing or stale
+library raises, so ``impl="hip"`` can never run on anything but the HIP kernels.
+"""
+import ctypes
+import os
+
+import torch
+
+ABI_VERSION = 2
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libfpa.so")
+
+FPA_F16, FPA_F32 = 0, 1
+FPA_OK, FPA_ERR_INVALID, FPA_ERR_UNSUPPORTED, FPA_ERR_HIP = 0, 1, 2, 3
+FPA_FWD_STATS, FPA_FWD_MAIN = 1, 2
+FPA_BWD_DELTA, FPA_BWD_KEYS, FPA_BWD_QUERIES, FPA_BWD_PHI, FPA_BWD_BETA = 1, 2, 4, 8, 16
+
+_i64 = ctypes.c_int64
+_vp = ctypes.c_void_p
+_S4 = _i64 * 4
+_S3 = _i64 * 3
+
+
+class FpaFwdArgs(ctypes.Structure):
+    _fields_ = [("B", _i64), ("H", _i64), ("T", _i64), ("D", _i64),
+                ("dtype", ctypes.c_int32), ("tau", ctypes.c_float),
+                ("q", _vp), ("sq", _S4), ("k", _vp), ("sk", _S4), ("v", _vp), ("sv", _S4),
+                ("phi", _vp), ("sphi", _S3), ("psi", _vp), ("spsi", _S3),
+                ("beta", _vp), ("o", _vp), ("so", _S4), ("lse", _vp), ("state", _vp),
+                ("phases", ctypes.c_int32)]
+
+
+class FpaBwdArgs(ctypes.Structure):
+    _fields_ = [("B", _i64), ("H", _i64), ("T", _i64), ("D", _i64),
+                ("dtype", ctypes.c_int32), ("tau", ctypes.c_float),
+                ("q", _vp), ("sq", _S4), ("k", _vp), ("sk", _S4), ("v", _vp), ("sv", _S4),
+                ("beta", _vp), ("o", _vp), ("so", _S4), ("dout", _vp), ("sdo", _S4),
+                ("lse", _vp), ("state", _vp),
+                ("dq", _vp), ("sdq", _S4), ("dk", _vp), ("sdk", _S4), ("dv", _vp), ("sdv", _S4),
+                ("dphi", _vp), ("dpsi", _vp), ("dbeta", _vp), ("workspace", _vp),
+                ("phases", ctypes.c_int32)]
+
+
+class FpaError(RuntimeError):
+    """A failed libfpa call (status code and message of fpa_last_error)."""
+
+    def __init__(self, code, msg):
+        super().__init__(msg)
+        self.code = code
+
+
+_LIB = None
+
+
+def lib():
+    """The loaded library; raises if it is not built or has the wrong ABI."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"libfpa.so is not built ({LIB_PATH}); run first-passage-attention_amd/build.py "
+                           "or __graft_entry__.build()")
+    L = ctypes.CDLL(LIB_PATH)
+    L.fpa_abi_version.restype = ctypes.c_int
+    L.fpa_last_error.restype = ctypes.c_char_p
+    for name in ("fpa_state_floats", "fpa_lse_floats"):
+        getattr(L, name).restype = _i64
+        getattr(L, name).argtypes = [_i64, _i64, _i64]
+    L.fpa_bwd_workspace_bytes.restype = _i64
+    L.fpa_bwd_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64, ctypes.c_int32]
+    L.fpa_fwd.restype = ctypes.c_int
+    L.fpa_fwd.argtypes = [ctypes.POINTER(FpaFwdArgs), _vp]
+    L.fpa_bwd.restype = ctypes.c_int
+    L.fpa_bwd.argtypes = [ctypes.POINTER(FpaBwdArgs), _vp]
+    if L.fpa_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"libfpa.so ABI {L.fpa_abi_version()} != {ABI_VERSION}: rebuild it")
+    _LIB = L
+    return L
+
+
+def check(rc):
+    if rc != FPA_OK:
+        msg = lib().fpa_last_error().decode()
+        if rc == FPA_ERR_INVALID:
+            raise ValueError(msg)
+        raise FpaError(rc, msg)
+
+
+def dtype_code(dt):
+    if dt == torch.float16:
+        return FPA_F16
+    if dt == torch.float32:
+        return FPA_F32
+    raise ValueError("q, k and v must all be fp16 or all fp32")
+
+
+def stream_of(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def ptr(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def strides4(t):
+    return _S4(*t.stride())
+
+
+def strides3(t):
+    return _S3(*t.stride())

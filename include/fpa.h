@@ -1,0 +1,128 @@
+/*
+ * fpa.h -- C ABI of the MI355X (gfx950) First Passage Attention library, libfpa.so.
+ *
+ * Plain C: device pointers, element strides and sizes; no torch or HIP types in
+ * the signatures (the stream is passed as the opaque hipStream_t pointer value,
+ * NULL = the default stream).  Every buffer is owned by the caller: the library
+ * never allocates device memory.  Calls only enqueue work on `stream` and never
+ * synchronise the host; they are re-entrant (no global mutable state besides the
+ * thread-local error message).
+ *
+ * Reference interfaces replaced (yliu-fort/first-passage-attention, kernel.py):
+ *   fpa_fwd  <- _forward (kernel.py:398-412) with _block_stats (387-395) and the
+ *               _stats / _fwd Triton kernels (83-100, 103-162);
+ *   fpa_bwd  <- _FirstPassageAttention.backward (kernel.py:424-451) with the
+ *               _bwd_delta/_bwd_kv/_bwd_dphi_diag/_bwd_q/_bwd_dphi kernels
+ *               (165-370) and the dbeta sum at kernel.py:450;
+ *   fpa_state_floats / fpa_bwd_workspace_bytes <- the scratch allocations of
+ *               kernel.py:390-392, 406-407, 430-436, sized so the caller owns them.
+ * Error behaviour mirrors the validation of first_passage_attention
+ * (kernel.py:467-486): invalid shapes or dtypes return FPA_ERR_INVALID with the
+ * reference's message available from fpa_last_error().
+ */
+#ifndef FPA_H
+#define FPA_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype of q, k, v, o, do, dq, dk, dv */
+#define FPA_F16 0
+#define FPA_F32 1
+
+/* phase bits (FpaFwdArgs.phases / FpaBwdArgs.phases) */
+#define FPA_FWD_STATS 1    /* block statistics of phi                      */
+#define FPA_FWD_MAIN 2     /* the forward kernel (o, lse)                  */
+#define FPA_BWD_DELTA 1    /* Delta_t = sum_d dO o                         */
+#define FPA_BWD_KEYS 2     /* key side: dk, dv, dpsi, dbeta partials, ...  */
+#define FPA_BWD_QUERIES 4  /* query side: dq, query-block soft-min sums    */
+#define FPA_BWD_PHI 8      /* dphi                                         */
+#define FPA_BWD_BETA 16    /* dbeta                                        */
+
+/* status codes */
+#define FPA_OK 0
+#define FPA_ERR_INVALID 1     /* invalid argument (shape, dtype, tau, stride)        */
+#define FPA_ERR_UNSUPPORTED 2 /* valid for the reference but not built (e.g. D > 128) */
+#define FPA_ERR_HIP 3         /* a HIP runtime call failed                            */
+
+/* Forward arguments.  Tensors are (B, H, T, D) for q/k/v/o and (B, H, T) for
+ * phi/psi, addressed with element strides s*[0..3] = (b, h, t, d); the d stride
+ * must be 1.  phi, psi, beta are float32; beta is (H,) contiguous.  lse and
+ * state are contiguous float32 buffers the forward fills and the backward reads:
+ * lse holds B*H*TP floats (TP = T rounded up to 64; base-2 log-sum-exp of each
+ * query row), state holds fpa_state_floats(B, H, T) floats (block statistics).  */
+typedef struct {
+    int64_t B, H, T, D;
+    int32_t dtype;
+    float tau;
+    const void *q;  int64_t sq[4];
+    const void *k;  int64_t sk[4];
+    const void *v;  int64_t sv[4];
+    const float *phi; int64_t sphi[3];
+    const float *psi; int64_t spsi[3];
+    const float *beta;
+    void *o;        int64_t so[4];
+    float *lse;
+    float *state;
+    int32_t phases;  /* 0: everything.  Otherwise a bitmask of the kernels to enqueue
+                        (FPA_FWD_STATS | FPA_FWD_MAIN), for per-kernel timing only. */
+} FpaFwdArgs;
+
+/* Backward arguments: the forward's inputs, o, lse and state, the incoming
+ * gradient do (strided like q), and the outputs.  dq, dk, dv have the dtype of
+ * q and strides sdq/sdk/sdv; dphi, dpsi are float32 (B, H, T) contiguous; dbeta is
+ * float32 (H,).  workspace is fpa_bwd_workspace_bytes(...) bytes of device memory,
+ * 256-byte aligned; its contents on entry do not matter.                        */
+typedef struct {
+    int64_t B, H, T, D;
+    int32_t dtype;
+    float tau;
+    const void *q;  int64_t sq[4];
+    const void *k;  int64_t sk[4];
+    const void *v;  int64_t sv[4];
+    const float *beta;
+    const void *o;  int64_t so[4];
+    const void *dout; int64_t sdo[4];
+    const float *lse;
+    const float *state;
+    void *dq;       int64_t sdq[4];
+    void *dk;       int64_t sdk[4];
+    void *dv;       int64_t sdv[4];
+    float *dphi;
+    float *dpsi;
+    float *dbeta;
+    void *workspace;
+    int32_t phases;  /* 0: everything.  Otherwise a bitmask of FPA_BWD_* kernels to enqueue,
+                        for per-kernel timing only: a partial run reads the workspace
+                        left by an earlier full run and leaves skipped outputs unwritten. */
+} FpaBwdArgs;
+
+/* Floats of the forward state (block statistics) for a (B, H, T) problem. */
+int64_t fpa_state_floats(int64_t B, int64_t H, int64_t T);
+
+/* Floats of lse for a (B, H, T) problem (B * H * TP). */
+int64_t fpa_lse_floats(int64_t B, int64_t H, int64_t T);
+
+/* Bytes of backward scratch for a (B, H, T, D) problem. */
+int64_t fpa_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D, int32_t dtype);
+
+/* Enqueue the forward on `stream` (a hipStream_t, NULL for the default stream). */
+int fpa_fwd(const FpaFwdArgs *args, void *stream);
+
+/* Enqueue the backward on `stream`. */
+int fpa_bwd(const FpaBwdArgs *args, void *stream);
+
+/* Message of the last failed call on this host thread ("" if none). */
+const char *fpa_last_error(void);
+
+/* ABI version (bumped whenever the structs above change). */
+int fpa_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FPA_H */

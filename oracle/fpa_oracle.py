@@ -1,0 +1,224 @@
+"""CPU oracle for First Passage Attention (FPA).
+
+TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import this module, and only as the
+checker (or, for ``cpu_baseline``, as the thing timed on the host CPU).  The
+product path (``impl="hip"``) never calls it.
+
+What it restates (reference ``kernel.py`` of yliu-fort/first-passage-attention):
+
+* ``kernel.py:3-8`` / ``README.md:11-13`` -- the definition.  For query ``t`` and
+  key ``s <= t`` of a head, ``b_ts = beta * min(0, min_{s<u<=t} phi_u - psi_s)``
+  with ``b_tt = 0``; ``o_t = sum_s softmax_s(q_t.k_s / sqrt(D) + b_ts) v_s``.
+* ``kernel.py:23-24`` -- arithmetic in float64 if any operand is float64, else
+  float32.
+* ``kernel.py:31-41`` -- the hard range minimum and the soft range minimum
+  ``-tau * log sum_{s<u<=t} exp(-phi_u / tau)`` (finite ``-1e30`` sentinel on the
+  empty ranges so that autograd never sees ``inf - inf``).
+* ``kernel.py:44-54`` -- the straight-through combination: the value is the hard
+  minimum, the gradient is the soft minimum's; ``clamp(max=0)`` passes the
+  gradient at equality.
+* ``kernel.py:57-64`` -- causal softmax attention with autocast off.
+
+Two independent formulations live here so that tests can pin one with the
+other: :func:`fpa_forward` / :func:`fpa_grads` (dense tensors + autograd, the
+reference's own formulation) and :func:`explicit_grads` (closed-form gradient
+formulas evaluated with loops, after ``test.py:66-84``).  :func:`bias_by_loops`
+and :func:`attention_by_loops` are brute-force restatements for tiny shapes.
+"""
+import math
+
+import numpy as np
+import torch
+
+LOG2E = 1.4426950408889634
+SENTINEL = 1e30  # kernel.py:39
+
+
+def compute_dtype(*xs):
+    """float64 if any operand is float64, else float32 (kernel.py:23-24)."""
+    return torch.float64 if any(x.dtype == torch.float64 for x in xs) else torch.float32
+
+
+def _strict_upper(T, device):
+    """mask[s, u] = u > s: the keys' ranges (s, t] start strictly after s."""
+    idx = torch.arange(T, device=device)
+    return idx[None, :] > idx[:, None]
+
+
+def range_min(phi):
+    """X[..., t, s] = min_{s<u<=t} phi_u, +inf where the range is empty (kernel.py:31-34)."""
+    T = phi.shape[-1]
+    grid = phi.unsqueeze(-2).expand(*phi.shape[:-1], T, T)           # [s, u] -> phi_u
+    grid = torch.where(_strict_upper(T, phi.device), grid, torch.full_like(grid, math.inf))
+    run = torch.cummin(grid, dim=-1).values                          # [s, t] = min over (s, t]
+    return run.transpose(-1, -2)
+
+
+def range_softmin(phi, tau):
+    """L[..., t, s] = -tau * log sum_{s<u<=t} exp(-phi_u/tau) (kernel.py:37-41)."""
+    T = phi.shape[-1]
+    grid = (-phi / tau).unsqueeze(-2).expand(*phi.shape[:-1], T, T)
+    grid = torch.where(_strict_upper(T, phi.device), grid, torch.full_like(grid, -SENTINEL))
+    return (-tau * torch.logcumsumexp(grid, dim=-1)).transpose(-1, -2)
+
+
+def first_passage_bias(phi, psi, beta, tau=1.0):
+    """(B, H, T, T) bias indexed [t, s]; straight-through soft-min gradient (kernel.py:44-54)."""
+    if not tau > 0:
+        raise ValueError("tau must be positive")
+    dt = compute_dtype(phi, psi)
+    phi, psi = phi.to(dt), psi.to(dt)
+    if torch.is_tensor(beta):
+        beta = beta.reshape(-1, 1, 1)
+    soft = range_softmin(phi, tau)
+    hard = range_min(phi).detach()
+    x = hard + (soft - soft.detach()) - psi.unsqueeze(-2)
+    return beta * torch.clamp(x, max=0.0)
+
+
+def causal_attention(q, k, v, bias):
+    """Causal softmax attention with an additive bias, autocast off (kernel.py:57-64)."""
+    dt = compute_dtype(q, bias)
+    T, D = q.shape[-2], q.shape[-1]
+    with torch.autocast(device_type=q.device.type, enabled=False):
+        logits = torch.matmul(q.to(dt), k.to(dt).transpose(-1, -2).contiguous()) / math.sqrt(D)
+        logits = logits + bias.to(dt)
+        causal = torch.ones(T, T, dtype=torch.bool, device=q.device).tril()
+        logits = logits.masked_fill(~causal, -math.inf)
+        return torch.matmul(torch.softmax(logits, dim=-1), v.to(dt)).to(q.dtype)
+
+
+def fpa_forward(q, k, v, phi, psi, beta, tau=1.0):
+    """Dense FPA output (the reference's ``impl="reference"`` path)."""
+    return causal_attention(q, k, v, first_passage_bias(phi, psi, beta, tau))
+
+
+def fpa_grads(q, k, v, phi, psi, beta, do, tau=1.0, dtype=torch.float64):
+    """(o, dq, dk, dv, dphi, dpsi, dbeta) of <o, do> by autograd, in ``dtype`` on the CPU.
+
+    beta may be a scalar or an (H,) tensor; dbeta is always returned with shape (H,).
+    """
+    H = q.shape[1]
+    b = beta if torch.is_tensor(beta) else torch.tensor(float(beta))
+    b = b.reshape(-1)
+    if b.numel() == 1:
+        b = b.expand(H)
+    args = [t.detach().cpu().to(dtype).requires_grad_() for t in (q, k, v, phi, psi)]
+    bb = b.detach().cpu().to(dtype).contiguous().requires_grad_()
+    o = fpa_forward(*args, bb, tau=tau)
+    grads = torch.autograd.grad(o, args + [bb], do.detach().cpu().to(dtype))
+    return [o.detach()] + [g.detach() for g in grads]
+
+
+# ----------------------------------------------------------------------------
+# Brute-force restatements used to pin the dense oracle on tiny shapes.
+# ----------------------------------------------------------------------------
+
+def bias_by_loops(phi, psi, beta):
+    """Loop-by-loop bias from the definition (after test.py:33-42)."""
+    phi, psi = np.asarray(phi, np.float64), np.asarray(psi, np.float64)
+    beta = np.broadcast_to(np.asarray(beta, np.float64).reshape(-1), (phi.shape[1],))
+    B, H, T = phi.shape
+    out = np.zeros((B, H, T, T))
+    for b in range(B):
+        for h in range(H):
+            for t in range(T):
+                for s in range(t):
+                    m = min(phi[b, h, s + 1:t + 1])
+                    out[b, h, t, s] = beta[h] * min(0.0, m - psi[b, h, s])
+    return out
+
+
+def attention_by_loops(q, k, v, bias):
+    """Row-by-row causal softmax with the bias (after test.py:51-63)."""
+    q, k, v, bias = (np.asarray(x, np.float64) for x in (q, k, v, bias))
+    B, H, T, D = q.shape
+    o = np.zeros_like(q)
+    for b in range(B):
+        for h in range(H):
+            for t in range(T):
+                z = k[b, h, :t + 1] @ q[b, h, t] / math.sqrt(D) + bias[b, h, t, :t + 1]
+                z = np.exp(z - z.max())
+                o[b, h, t] = (z / z.sum()) @ v[b, h, :t + 1]
+    return o
+
+
+def explicit_grads(q, k, v, phi, psi, beta, do, tau=1.0):
+    """Closed-form gradients, loops over (t, s) for the bias terms (after test.py:66-84).
+
+    Softmax backward: dS = P * (dP - rowsum(dO * O)); dq = dS k / sqrt(D);
+    dk = dS^T q / sqrt(D); dv = P^T dO.  Bias terms, with gate g_ts = [x_ts <= 0]
+    and x_ts = min_{s<u<=t} phi_u - psi_s:
+      dpsi_s -= beta * g * dS_ts;  dbeta += min(0, x_ts) * dS_ts;
+      dphi_u += beta * g * dS_ts * softmax_{u' in (s, t]}(-phi_u'/tau)[u].
+    """
+    q, k, v, phi, psi, do = (np.asarray(x, np.float64) for x in (q, k, v, phi, psi, do))
+    B, H, T, D = q.shape
+    beta = np.broadcast_to(np.asarray(beta, np.float64).reshape(-1), (H,))
+    bias = bias_by_loops(phi, psi, beta)
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+    dphi, dpsi, dbeta = np.zeros_like(phi), np.zeros_like(psi), np.zeros(H)
+    o = np.zeros_like(q)
+    for b in range(B):
+        for h in range(H):
+            z = q[b, h] @ k[b, h].T / math.sqrt(D) + bias[b, h]
+            z = np.where(np.tril(np.ones((T, T), bool)), z, -np.inf)
+            p = np.exp(z - z.max(-1, keepdims=True))
+            p /= p.sum(-1, keepdims=True)
+            o[b, h] = p @ v[b, h]
+            dp = do[b, h] @ v[b, h].T
+            ds = p * (dp - (do[b, h] * o[b, h]).sum(-1, keepdims=True))
+            dq[b, h] = ds @ k[b, h] / math.sqrt(D)
+            dk[b, h] = ds.T @ q[b, h] / math.sqrt(D)
+            dv[b, h] = p.T @ do[b, h]
+            for t in range(T):
+                for s in range(t):
+                    rng = phi[b, h, s + 1:t + 1]
+                    x = rng.min() - psi[b, h, s]
+                    gate = 1.0 if x <= 0 else 0.0
+                    w = np.exp(-(rng - rng.min()) / tau)
+                    w /= w.sum()
+                    dphi[b, h, s + 1:t + 1] += beta[h] * gate * ds[t, s] * w
+                    dpsi[b, h, s] -= beta[h] * gate * ds[t, s]
+                    dbeta[h] += min(0.0, x) * ds[t, s]
+    return [o, dq, dk, dv, dphi, dpsi, dbeta]
+
+
+# ----------------------------------------------------------------------------
+# Seeded inputs (the distributions of BASELINE.json / reference test.py:108-117)
+# ----------------------------------------------------------------------------
+
+def make_inputs(B, H, T, D, dtype=torch.float16, seed=0, phi_scale=1.0, ties=False,
+                psi_noise=0.5, beta="uniform", drift=0.0):
+    """Seeded CPU inputs (q, k, v, phi, psi, beta, do).
+
+    q, k, v, do ~ N(0, 1) cast to ``dtype``; phi = phi_scale * cumsum N(0, 1) - drift * t
+    (rounded when ``ties``); psi = phi + psi_noise * N(0, 1); beta = U(0,1) + 0.5
+    ("uniform"), ones ("ones") or softplus(N(0, 1)) ("softplus").
+    """
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = (torch.randn(B, H, T, D, generator=g).to(dtype) for _ in range(3))
+    phi = torch.randn(B, H, T, generator=g).cumsum(-1) * phi_scale
+    if drift:
+        phi = phi - drift * torch.arange(T, dtype=phi.dtype)
+    if ties:
+        phi = torch.round(phi)
+    psi = phi + psi_noise * torch.randn(B, H, T, generator=g)
+    if beta == "uniform":
+        b = torch.rand(H, generator=g) + 0.5
+    elif beta == "ones":
+        b = torch.ones(H)
+    elif beta == "softplus":
+        b = torch.nn.functional.softplus(torch.randn(H, generator=g))
+    else:
+        raise ValueError(beta)
+    do = torch.randn(B, H, T, D, generator=g).to(dtype)
+    return q, k, v, phi, psi, b, do
+
+
+def rel_err(x, ref):
+    """max |x - ref| / max |ref| (reference test.py:120-121)."""
+    x = torch.as_tensor(x).double().cpu()
+    ref = torch.as_tensor(ref).double().cpu()
+    return ((x - ref).abs().max() / ref.abs().max().clamp(min=1e-30)).item()

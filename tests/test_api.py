@@ -1,0 +1,190 @@
+"""CPU tests of the host side: the C ABI library, the Python surface and the dense path.
+
+No GPU work here: the library is loaded and its exports and size queries are checked,
+argument validation is exercised (it returns before any launch), and the
+``impl="reference"`` path and the layer are checked against the oracle on the CPU.
+"""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+import fpa
+from fpa import _lib
+from oracle import fpa_oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fpa.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(fpa_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    names = declared_functions()
+    assert names, "no functions parsed from include/fpa.h"
+    for n in names:
+        assert hasattr(L, n), n
+    assert L.fpa_abi_version() == _lib.ABI_VERSION
+
+
+def test_struct_layout_matches_header(tmp_path):
+    """The ctypes mirrors have the layout gcc gives the structs of include/fpa.h."""
+    import shutil
+    import subprocess
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    lines = []
+    for cls, cname in ((_lib.FpaFwdArgs, "FpaFwdArgs"), (_lib.FpaBwdArgs, "FpaBwdArgs")):
+        lines.append(f'printf("{cname} sizeof %zu\\n", sizeof({cname}));')
+        for n, _ in cls._fields_:
+            lines.append(f'printf("{cname} {n} %zu\\n", offsetof({cname}, {n}));')
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "fpa.h"\nint main(void){\n'
+                   + "\n".join(lines) + "\nreturn 0;}\n")
+    exe = tmp_path / "layout"
+    subprocess.run([cc, "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    for line in filter(None, out):
+        cname, field, val = line.split()
+        cls = getattr(_lib, cname)
+        got = ctypes.sizeof(cls) if field == "sizeof" else getattr(cls, field).offset
+        assert got == int(val), (cname, field, got, val)
+
+
+def test_size_queries():
+    L = _lib.lib()
+    B, H, T = 2, 3, 100
+    TP, NB = 128, 2
+    assert L.fpa_lse_floats(B, H, T) == B * H * TP
+    assert L.fpa_state_floats(B, H, T) == 6 * B * H * TP + 2 * B * H * NB
+    ws = L.fpa_bwd_workspace_bytes(B, H, T, 64, 0)
+    assert ws % 256 == 0 and ws >= 4 * (3 * B * H * TP + B * H * NB * 64 * 64)
+
+
+@pytest.mark.parametrize("field,value,code,msg", [
+    ("tau", 0.0, _lib.FPA_ERR_INVALID, "tau must be positive"),
+    ("D", 24, _lib.FPA_ERR_INVALID, "the head dimension and the block must be powers of two >= 16"),
+    ("dtype", 7, _lib.FPA_ERR_INVALID, "q, k and v must all be fp16 or all fp32"),
+    ("D", 512, _lib.FPA_ERR_UNSUPPORTED, "head dimension 512 is not built"),
+    ("T", 0, _lib.FPA_ERR_INVALID, "q, k and v must have the same shape (B, H, T, D)"),
+])
+def test_c_abi_validation(field, value, code, msg):
+    L = _lib.lib()
+    a = _lib.FpaFwdArgs()
+    a.B, a.H, a.T, a.D, a.dtype, a.tau = 1, 1, 16, 64, 0, 1.0
+    setattr(a, field, value)
+    assert L.fpa_fwd(a, None) == code
+    assert msg in L.fpa_last_error().decode()
+
+
+def test_c_abi_rejects_unaligned_rows():
+    L = _lib.lib()
+    a = _lib.FpaFwdArgs()
+    a.B, a.H, a.T, a.D, a.dtype, a.tau = 1, 1, 16, 64, 0, 1.0
+    a.q = a.k = a.v = a.o = ctypes.c_void_p(16 * 1024)
+    a.sq[:] = a.sk[:] = a.sv[:] = a.so[:] = (1024, 1024, 64, 1)
+    a.sq[2] = 3   # t stride not a multiple of 8 halves
+    assert L.fpa_fwd(a, None) == _lib.FPA_ERR_INVALID
+    assert "16-byte aligned" in L.fpa_last_error().decode()
+
+
+def test_python_validation_order_and_messages():
+    q = torch.zeros(1, 2, 8, 16, dtype=torch.float16)
+    phi = psi = torch.zeros(1, 2, 8)
+    beta = torch.ones(2)
+    f = fpa.first_passage_attention
+    with pytest.raises(ValueError, match="unknown implementation 'cuda'"):
+        f(q, q, q, phi, psi, beta, impl="cuda")
+    with pytest.raises(ValueError, match="same shape"):
+        f(q, q[:, :1], q, phi, psi, beta, impl="hip")
+    with pytest.raises(ValueError, match="fp16 or all fp32"):
+        f(q, q.float(), q, phi, psi, beta, impl="hip")
+    with pytest.raises(ValueError, match=r"phi and psi must have shape \(B, H, T\)"):
+        f(q, q, q, phi[:, :1], psi, beta, impl="hip")
+    with pytest.raises(ValueError, match="powers of two"):
+        f(q, q, q, phi, psi, beta, impl="hip", block=24)
+    with pytest.raises(ValueError, match=r"beta must have shape \(H,\)"):
+        f(q, q, q, phi, psi, torch.ones(3), impl="hip")
+    with pytest.raises(ValueError, match="tau must be positive"):
+        f(q, q, q, phi, psi, beta, tau=-1.0, impl="hip")
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        f(q, q, q, phi, psi, beta, impl="hip")
+    with pytest.raises(ValueError, match="multiple of n_heads"):
+        fpa.FirstPassageAttention(30, 4)
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_dense_path_matches_the_oracle(dtype):
+    q, k, v, phi, psi, beta, do = O.make_inputs(2, 3, 40, 8, dtype=dtype, seed=3, phi_scale=5.0)
+    a = [t.to(dtype if t.dim() == 4 else torch.float64).clone().requires_grad_() for t in (q, k, v, phi, psi)]
+    b = beta.double().requires_grad_()
+    o = fpa.first_passage_attention(*a, b, tau=0.6, impl="reference")
+    got = [o] + list(torch.autograd.grad(o, a + [b], do.to(dtype)))
+    ref = O.fpa_grads(q, k, v, phi, psi, beta, do, tau=0.6)
+    tol = 1e-12 if dtype == torch.float64 else 2e-5
+    for name, x, r in zip(("o", "dq", "dk", "dv", "dphi", "dpsi", "dbeta"), got, ref):
+        assert O.rel_err(x.detach(), r) <= tol, name
+
+
+def test_impl_none_on_cpu_is_the_dense_path():
+    q, k, v, phi, psi, beta, _ = O.make_inputs(1, 2, 20, 16, dtype=torch.float64, seed=4)
+    o1 = fpa.first_passage_attention(q, k, v, phi, psi, beta)
+    o2 = fpa.first_passage_attention(q, k, v, phi, psi, beta, impl="reference")
+    assert torch.equal(o1, o2)
+
+
+def test_kernel_module_alias():
+    import kernel
+    assert kernel.first_passage_attention is fpa.first_passage_attention
+    assert kernel.FirstPassageAttention is fpa.FirstPassageAttention
+
+
+def _layer(impl, d_model=64, n_heads=4, T=50, seed=0):
+    torch.manual_seed(seed)
+    layer = fpa.FirstPassageAttention(d_model, n_heads, impl=impl)
+    x = torch.randn(2, T, d_model, generator=torch.Generator().manual_seed(seed + 1))
+    return layer, x
+
+
+def test_layer_causal():
+    """After test.py:184-190."""
+    layer, x = _layer("reference")
+    t0 = 30
+    x2 = x.clone()
+    x2[:, t0 + 1:] = torch.randn(x2[:, t0 + 1:].shape) * 5
+    with torch.no_grad():
+        assert torch.allclose(layer(x)[:, :t0 + 1], layer(x2)[:, :t0 + 1], rtol=0, atol=1e-6)
+
+
+def test_layer_gradients():
+    """After test.py:193-197."""
+    layer, x = _layer("reference")
+    layer(x).square().mean().backward()
+    for name, p in layer.named_parameters():
+        assert p.grad is not None and torch.isfinite(p.grad).all() and p.grad.abs().max() > 0, name
+
+
+def test_field_initial_beta():
+    f = fpa.Field(16, 3, beta_init=0.7)
+    _, _, beta = f(torch.randn(1, 5, 16))
+    assert torch.allclose(beta, torch.full((3,), 0.7), atol=1e-6)
+
+
+def test_field_matches_definition():
+    """phi = cumsum(delta) + g, psi = cumsum(delta) + h from one fp32 projection."""
+    torch.manual_seed(5)
+    f = fpa.Field(12, 2)
+    x = torch.randn(2, 9, 12)
+    phi, psi, _ = f(x)
+    lin = x @ f.proj.weight.T + f.proj.bias
+    d, g, h = lin.view(2, 9, 3, 2).permute(2, 0, 3, 1)
+    assert torch.allclose(phi, d.cumsum(-1) + g, atol=1e-5)
+    assert torch.allclose(psi, d.cumsum(-1) + h, atol=1e-5)

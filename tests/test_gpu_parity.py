@@ -1,0 +1,181 @@
+"""Parity of the HIP kernels (impl="hip", libfpa.so) with the float64 CPU oracle.
+
+Mirrors the kernel tests of the reference (test.py:134-214): every output and gradient
+must be finite, have the reference's dtype (o, dq, dk, dv in the input dtype; dphi,
+dpsi, dbeta float32) and be within max|x - ref| / max|ref| <= 2e-3 (fp16; 1e-2 for
+dbeta) or 2e-4 (fp32) of the float64 oracle; repeated runs must be bit-identical.
+"""
+import sys
+
+import pytest
+import torch
+
+from oracle import fpa_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+NAMES = ("o", "dq", "dk", "dv", "dphi", "dpsi", "dbeta")
+TOL = {torch.float16: 2e-3, torch.float32: 2e-4}
+TOL_DBETA_FP16 = 1e-2
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def fpa():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    import fpa as m
+    from fpa import _lib
+    _lib.lib()  # loud failure if libfpa.so is missing
+    return m
+
+
+def run_hip(fpa, q, k, v, phi, psi, beta, do, tau=1.0):
+    dev = "cuda"
+    a = [t.to(dev).clone().requires_grad_() for t in (q, k, v, phi, psi, beta)]
+    o = fpa.first_passage_attention(*a, tau=tau, impl="hip")
+    grads = torch.autograd.grad(o, a, do.to(dev))
+    torch.cuda.synchronize()
+    return [o.detach().cpu()] + [g.detach().cpu() for g in grads]
+
+
+def check(kern, ref, dtype):
+    for name, x, r in zip(NAMES, kern, ref):
+        want_dtype = dtype if name in ("o", "dq", "dk", "dv") else torch.float32
+        assert x.dtype == want_dtype, (name, x.dtype)
+        assert torch.isfinite(x).all(), name
+        tol = TOL_DBETA_FP16 if (name == "dbeta" and dtype == torch.float16) else TOL[dtype]
+        err = O.rel_err(x, r)
+        assert err <= tol, (name, err)
+
+
+# (B, H, T, D, phi_scale, ties, dtype, seed, tau): the reference's CASES (test.py:134-147)
+# plus head dimensions 16..128 in both dtypes, ragged and tiny T, and tau != 1.
+CASES = [
+    (1, 2, 64, 64, 1.0, False, torch.float16, 100, 1.0),
+    (2, 3, 100, 64, 1.0, False, torch.float16, 101, 1.0),
+    (1, 2, 128, 64, 1.0, False, torch.float16, 102, 1.0),
+    (1, 2, 96, 64, 40.0, False, torch.float16, 103, 1.0),
+    (1, 2, 96, 64, 1.0, True, torch.float16, 104, 1.0),
+    (1, 2, 80, 32, 1.0, False, torch.float16, 110, 1.0),
+    (1, 2, 100, 64, 1.0, False, torch.float32, 111, 1.0),
+    (1, 2, 96, 16, 40.0, False, torch.float32, 112, 1.0),
+    (2, 4, 512, 64, 1.0, False, torch.float16, 105, 1.0),
+    (1, 2, 2048, 64, 1.0, False, torch.float16, 106, 1.0),
+    (1, 2, 2048, 64, 1.0, False, torch.float32, 200, 1.0),
+    (1, 2, 1000, 64, 40.0, False, torch.float32, 201, 1.0),
+    (1, 2, 300, 128, 1.0, False, torch.float16, 300, 1.0),
+    (1, 2, 300, 128, 1.0, False, torch.float32, 301, 1.0),
+    (1, 3, 257, 16, 1.0, False, torch.float16, 302, 1.0),
+    (1, 1, 1, 32, 1.0, False, torch.float16, 303, 1.0),
+    (1, 2, 7, 32, 1.0, False, torch.float32, 304, 1.0),
+    (2, 2, 65, 64, 3.0, True, torch.float16, 305, 0.7),
+    (1, 2, 700, 32, 1.0, False, torch.float16, 306, 2.0),
+]
+
+
+@pytest.mark.parametrize("B,H,T,D,scale,ties,dtype,seed,tau", CASES)
+def test_kernel_matches_the_oracle(fpa, B, H, T, D, scale, ties, dtype, seed, tau):
+    _say(f"[parity] B={B} H={H} T={T} D={D} scale={scale} ties={ties} {dtype} seed={seed} tau={tau}")
+    q, k, v, phi, psi, beta, do = O.make_inputs(B, H, T, D, dtype=dtype, seed=seed, phi_scale=scale, ties=ties)
+    kern = run_hip(fpa, q, k, v, phi, psi, beta, do, tau)
+    ref = O.fpa_grads(q, k, v, phi, psi, beta, do, tau=tau)
+    check(kern, ref, dtype)
+
+
+def test_kernel_temperature(fpa):
+    """After test.py:162-167: tau = 0.25, fp32."""
+    _say("[parity] temperature tau=0.25")
+    q, k, v, phi, psi, beta, do = O.make_inputs(1, 2, 72, 32, dtype=torch.float32, seed=11)
+    check(run_hip(fpa, q, k, v, phi, psi, beta, do, 0.25), O.fpa_grads(q, k, v, phi, psi, beta, do, tau=0.25),
+          torch.float32)
+
+
+def test_kernel_deterministic(fpa):
+    """After test.py:170-174: two runs are bit-identical (no unordered atomics)."""
+    _say("[determinism] B=2 H=2 T=96 D=32 fp16, and B=1 H=2 T=600 D=64 fp16")
+    for shape, seed in (((2, 2, 96, 32), 12), ((1, 2, 600, 64), 13)):
+        inp = O.make_inputs(*shape, seed=seed)
+        runs = [run_hip(fpa, *inp) for _ in range(2)]
+        assert all(torch.equal(x, y) for x, y in zip(*runs))
+
+
+def test_negative_and_zero_beta(fpa):
+    """beta <= 0 flips / removes the bias; the kernels take the sign per head."""
+    _say("[parity] beta = (-0.7, 0, 1.3)")
+    q, k, v, phi, psi, _, do = O.make_inputs(1, 3, 150, 32, dtype=torch.float32, seed=31)
+    beta = torch.tensor([-0.7, 0.0, 1.3])
+    check(run_hip(fpa, q, k, v, phi, psi, beta, do), O.fpa_grads(q, k, v, phi, psi, beta, do), torch.float32)
+
+
+def test_scalar_beta_and_strided_views(fpa):
+    """beta given as a Python float; q, k, v as permuted views of one (B, T, 3, H, D) tensor."""
+    _say("[parity] scalar beta, permuted q/k/v views")
+    B, H, T, D = 2, 3, 130, 32
+    g = torch.Generator().manual_seed(41)
+    qkv = torch.randn(B, T, 3, H, D, generator=g).half()
+    q, k, v = qkv.permute(2, 0, 3, 1, 4)
+    _, _, _, phi, psi, _, do = O.make_inputs(B, H, T, D, seed=42)
+    dev = "cuda"
+    qkv_d = qkv.to(dev).requires_grad_()
+    qd, kd, vd = qkv_d.permute(2, 0, 3, 1, 4)
+    pd, sd = phi.to(dev).requires_grad_(), psi.to(dev).requires_grad_()
+    o = fpa.first_passage_attention(qd, kd, vd, pd, sd, 0.8, impl="hip")
+    dqkv, dphi, dpsi = torch.autograd.grad(o, [qkv_d, pd, sd], do.to(dev))
+    ref = O.fpa_grads(q, k, v, phi, psi, torch.tensor(0.8), do)
+    dq, dk, dv = dqkv.cpu().permute(2, 0, 3, 1, 4)
+    check([o.detach().cpu(), dq, dk, dv, dphi.cpu(), dpsi.cpu(), ref[6]], ref, torch.float16)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_bench_shape_heads(fpa, dtype):
+    """The north-star shape B4 H12 T2048 D64 runs whole on the GPU; two of its 48 heads are
+    checked against the oracle (FPA is independent per head)."""
+    _say(f"[parity] B4 H12 T2048 D64 {dtype}, heads (0,0) and (3,11)")
+    B, H, T, D = 4, 12, 2048, 64
+    q, k, v, phi, psi, _, do = O.make_inputs(B, H, T, D, dtype=dtype, seed=0, psi_noise=1.0)
+    beta = torch.ones(H)
+    kern = run_hip(fpa, q, k, v, phi, psi, beta, do)
+    for b, h in ((0, 0), (3, 11)):
+        sl = lambda t: t[b:b + 1, h:h + 1]  # noqa: E731
+        ref = O.fpa_grads(sl(q), sl(k), sl(v), sl(phi), sl(psi), beta[h:h + 1], sl(do))
+        got = [sl(x) for x in kern[:6]]
+        for name, x, r in zip(NAMES[:6], got, ref[:6]):
+            assert torch.isfinite(x).all(), name
+            assert O.rel_err(x, r) <= TOL[dtype], (name, b, h, O.rel_err(x, r))
+    assert torch.isfinite(kern[6]).all()
+
+
+def test_layer_kernel_matches_the_reference(fpa):
+    """After test.py:200-214: the FirstPassageAttention layer, hip vs the dense path, fp32."""
+    _say("[layer] fp32 hip vs reference")
+    out = []
+    for impl in ("hip", "reference"):
+        torch.manual_seed(0)
+        layer = fpa.FirstPassageAttention(64, 4, impl=impl).cuda()
+        x = torch.randn(2, 50, 64, generator=torch.Generator().manual_seed(1)).cuda()
+        y = layer(x)
+        loss = y.float().square().mean()
+        out.append([y.detach().float()] + list(torch.autograd.grad(loss, list(layer.parameters()))))
+    for a, b in zip(*out):
+        assert ((a - b).norm() / b.norm()).item() <= 1e-4
+
+
+def test_layer_kernel_fp16_autocast(fpa):
+    """After test.py:200-214 with amp: fp16 autocast, relative norm <= 5e-3."""
+    _say("[layer] fp16 autocast hip vs fp32 reference")
+    out = []
+    for impl, amp in (("hip", True), ("reference", True)):
+        torch.manual_seed(0)
+        layer = fpa.FirstPassageAttention(64, 4, impl=impl).cuda()
+        x = torch.randn(2, 50, 64, generator=torch.Generator().manual_seed(1)).cuda()
+        with torch.autocast("cuda", dtype=torch.float16, enabled=amp):
+            y = layer(x)
+        loss = y.float().square().mean()
+        out.append([y.detach().float()] + list(torch.autograd.grad(loss, list(layer.parameters()))))
+    for a, b in zip(*out):
+        assert ((a - b).norm() / b.norm()).item() <= 5e-3

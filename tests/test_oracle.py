@@ -1,0 +1,121 @@
+"""Pins the CPU oracle (oracle/fpa_oracle.py) against brute force, closed forms and invariants.
+
+Mirrors the definition tests of the reference (test.py:45-105): the oracle is only
+trusted because these pass.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fpa_oracle as O
+
+
+def random_field(B, H, T, seed, ties=False):
+    g = torch.Generator().manual_seed(seed)
+    phi = torch.randn(B, H, T, generator=g, dtype=torch.float64).cumsum(-1)
+    if ties:
+        phi = torch.round(phi)
+    psi = phi + 0.5 * torch.randn(B, H, T, generator=g, dtype=torch.float64)
+    beta = torch.rand(H, generator=g, dtype=torch.float64) + 0.5
+    return phi, psi, beta
+
+
+@pytest.mark.parametrize("ties", [False, True])
+def test_bias_is_the_definition(ties):
+    phi, psi, beta = random_field(2, 3, 12, seed=1 + ties, ties=ties)
+    got = O.first_passage_bias(phi, psi, beta).numpy()
+    assert np.array_equal(got, O.bias_by_loops(phi, psi, beta))
+
+
+def test_attention_is_softmax_with_the_bias():
+    B, H, T, D = 2, 3, 10, 8
+    g = torch.Generator().manual_seed(3)
+    q, k, v = (torch.randn(B, H, T, D, generator=g, dtype=torch.float64) for _ in range(3))
+    phi, psi, beta = random_field(B, H, T, seed=4)
+    want = O.attention_by_loops(q, k, v, O.bias_by_loops(phi, psi, beta))
+    got = O.fpa_forward(q, k, v, phi, psi, beta).numpy()
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("tau,scale,ties", [(0.7, 1.0, False), (1.0, 40.0, False), (0.25, 1.0, True)])
+def test_gradients_match_the_closed_form(tau, scale, ties):
+    B, H, T, D = 1, 2, 11, 4
+    q, k, v, phi, psi, beta, do = O.make_inputs(B, H, T, D, dtype=torch.float64, seed=5,
+                                                phi_scale=scale, ties=ties)
+    got = O.fpa_grads(q, k, v, phi, psi, beta, do, tau=tau)
+    want = O.explicit_grads(q, k, v, phi, psi, beta, do, tau=tau)
+    for name, a, b in zip(("o", "dq", "dk", "dv", "dphi", "dpsi", "dbeta"), got, want):
+        assert np.allclose(a.numpy(), b, rtol=1e-9, atol=1e-11), name
+
+
+def test_gradient_of_the_bias_alone():
+    """After reference test.py:66-84: d<bias, G>/d(phi, psi, beta) against loops."""
+    B, H, T, tau = 1, 2, 9, 0.7
+    phi, psi, beta = random_field(B, H, T, seed=5)
+    G = torch.randn(B, H, T, T, generator=torch.Generator().manual_seed(6), dtype=torch.float64)
+    args = [t.clone().requires_grad_() for t in (phi, psi, beta)]
+    dphi, dpsi, dbeta = torch.autograd.grad((O.first_passage_bias(*args, tau=tau) * G).sum(), args)
+    e_phi, e_psi, e_beta = np.zeros((B, H, T)), np.zeros((B, H, T)), np.zeros(H)
+    for h in range(H):
+        for t in range(T):
+            for s in range(t):
+                rng = phi[0, h, s + 1:t + 1].numpy()
+                x = rng.min() - psi[0, h, s].item()
+                gate = 1.0 if x <= 0 else 0.0
+                w = np.exp(-(rng - rng.min()) / tau)
+                e_phi[0, h, s + 1:t + 1] += beta[h].item() * gate * G[0, h, t, s].item() * w / w.sum()
+                e_psi[0, h, s] -= beta[h].item() * gate * G[0, h, t, s].item()
+                e_beta[h] += min(0.0, x) * G[0, h, t, s].item()
+    for got, want in ((dphi, e_phi), (dpsi, e_psi), (dbeta, e_beta)):
+        assert np.allclose(got.numpy(), want, rtol=1e-10, atol=1e-12)
+
+
+def test_causal():
+    B, H, T, D, t0 = 1, 2, 16, 8, 9
+    g = torch.Generator().manual_seed(7)
+    q, k, v = (torch.randn(B, H, T, D, generator=g, dtype=torch.float64) for _ in range(3))
+    phi, psi, beta = random_field(B, H, T, seed=8)
+    o = O.fpa_forward(q, k, v, phi, psi, beta)
+    later = [t.clone() for t in (q, k, v, phi, psi)]
+    for t in later:
+        t[:, :, t0 + 1:] = torch.randn(t[:, :, t0 + 1:].shape, generator=g, dtype=torch.float64) * 10
+    o2 = O.fpa_forward(*later, beta)
+    assert torch.equal(o[:, :, :t0 + 1], o2[:, :, :t0 + 1])
+
+
+def test_bias_never_rises():
+    phi, psi, beta = random_field(2, 3, 24, seed=10)
+    b = O.first_passage_bias(phi, psi, beta)
+    T = phi.shape[-1]
+    keys = torch.ones(T, T, dtype=torch.bool).tril()[:-1]
+    assert (b[:, :, 1:][..., keys] <= b[:, :, :-1][..., keys]).all()
+
+
+def test_zero_beta_is_plain_causal_attention():
+    """beta = 0 removes the bias: the output is causal softmax attention (torch SDPA)."""
+    q, k, v, phi, psi, _, _ = O.make_inputs(2, 3, 33, 16, dtype=torch.float64, seed=21)
+    o = O.fpa_forward(q, k, v, phi, psi, torch.zeros(3, dtype=torch.float64))
+    want = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True)
+    assert torch.allclose(o, want, rtol=1e-12, atol=1e-12)
+
+
+def test_small_tau_gradient_goes_to_the_argmin():
+    """As tau -> 0 the soft-min weight concentrates on the argmin of phi over (s, t]."""
+    phi = torch.tensor([[[0.0, 3.0, 1.0, 2.0, -1.0, 0.5]]], dtype=torch.float64)
+    psi = torch.full_like(phi, 10.0)          # every gate open
+    beta = torch.ones(1, dtype=torch.float64)
+    G = torch.zeros(1, 1, 6, 6, dtype=torch.float64)
+    G[0, 0, 3, 0] = 1.0                       # pair (t=3, s=0): range (0, 3] = {3, 1, 2}, argmin u=2
+    p = phi.clone().requires_grad_()
+    (dphi,) = torch.autograd.grad((O.first_passage_bias(p, psi, beta, tau=1e-3) * G).sum(), [p])
+    want = torch.zeros_like(phi)
+    want[0, 0, 2] = 1.0
+    assert torch.allclose(dphi, want, atol=1e-12)
+
+
+def test_tau_must_be_positive():
+    phi, psi, beta = random_field(1, 1, 4, seed=0)
+    with pytest.raises(ValueError, match="tau must be positive"):
+        O.first_passage_bias(phi, psi, beta, tau=0.0)
