@@ -219,8 +219,8 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_kv_kernel(BwdParams p) {
     gsum += __shfl_xor(gsum, 32, 64);
     Wacc += __shfl_xor(Wacc, 32, 64);
     const float dbw = wave_sum(dbacc);
+    if (lane == 0) p.dbp[((int64_t)bh * p.NKV + kt) * 4 + w] = dbw;  // 0 for waves past T
     if (!wave_active) return;
-    if (lane == 0) p.dbp[((int64_t)bh * p.NKV + kt) * 4 + w] = dbw;
     if (g == 0 && s < p.TP) p.wsum[rowbase + s] = Wacc;
     if (g == 0 && s_valid) p.dpsi[(int64_t)bh * p.T + s] = -beta * gsum;
     if (!s_valid) return;
