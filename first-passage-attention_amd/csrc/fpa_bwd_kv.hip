@@ -2,10 +2,11 @@
 //
 // Reference behaviour: _bwd_delta (kernel.py:165-174) and _bwd_kv (kernel.py:177-265)
 // of yliu-fort/first-passage-attention.  gfx950 design: a workgroup of 4 waves owns
-// 128 keys (32 per wave, one key per lane column) and streams 32-query tiles from
-// the diagonal to T through LDS (Q and dO both row-major and transposed).  Each
-// wave computes S = Q K^T and dP = dO V^T with K, V held in registers, then
-// dV^T += dO^T P and dK^T += Q^T dS on the 32x32 MFMA.  Per key it also reduces
+// 128 keys (32 per wave, one key per lane column) and streams 64-query blocks from
+// the diagonal to T through double-buffered LDS (register prefetch of the next block,
+// one barrier per block).  Each wave computes S = Q K^T and dP = dO V^T with K, V
+// held in registers, then dV^T += dO^T P and dK^T += Q^T dS on the 32x32 MFMA (dO^T
+// and Q^T read from the row-major tiles with LDS transpose reads).  Per key it reduces
 //   dpsi_s  = -beta * sum_t g_ts                       (g = [x <= 0] dS, strict t > s)
 //   dbeta   = sum_{t>s} dS_ts min(0, x_ts)             (per-wave partials, summed later)
 //   W_s     = sum_{t outside blk(s)} g_ts 2^{C_s} / Z_ts   (key-block soft-min sums)
@@ -46,22 +47,21 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_prep_kernel(BwdParams p) {
     if (part == 0 && row < p.TP) p.delta[(int64_t)bh * p.TP + row] = acc;
 }
 
-template <typename T, int D>
-__global__ void __launch_bounds__(NTHREADS) fpa_bwd_kv_kernel(BwdParams p) {
-    constexpr int BK = 128, BQ = 32;
+template <typename T, int D, int WPE>
+__global__ void __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+fpa_bwd_kv_kernel(BwdParams p) {
+    constexpr int BK = 128, BQ = 64;   // keys per workgroup, queries per iteration (one block)
     constexpr int DT = D < 32 ? 32 : D;
     constexpr int NDT = DT / 32;
-    constexpr int PQ = D + (sizeof(T) == 2 ? 8 : 4);  // row-major tile pitch
-    constexpr int PT = BQ + 4;                          // transposed tile pitch
-    __shared__ __attribute__((aligned(16))) T Qs[BQ * PQ];
-    __shared__ __attribute__((aligned(16))) T dOs[BQ * PQ];
-    __shared__ __attribute__((aligned(16))) T QT[DT * PT];
-    __shared__ __attribute__((aligned(16))) T dOT[DT * PT];
-    __shared__ float rLSE[BQ], rDEL[BQ], rPRE[BQ], rPREL[BQ];
+    constexpr int PQ = D + (sizeof(T) == 2 ? 8 : 4);  // tile pitch (elements)
+    constexpr int TS = BQ * PQ;
+    __shared__ __attribute__((aligned(16))) T Qs[2 * TS + (DT - D)];
+    __shared__ __attribute__((aligned(16))) T dOs[2 * TS + (DT - D)];
+    __shared__ __attribute__((aligned(16))) float rLSE[2][BQ], rDEL[2][BQ], rPRE[2][BQ], rPREL[2][BQ];
     __shared__ float kPHI[BK];
 
     const int tid = threadIdx.x, w = tid / 64, lane = tid % 64, g = lane / 32, c = lane % 32;
-    const int kt = blockIdx.x;  // heaviest (most query tiles) first
+    const int kt = blockIdx.x;  // heaviest (most query blocks) first
     const int bh = blockIdx.y, b = bh / p.H, h = bh % p.H;
     const int k0 = kt * BK, kw0 = k0 + 32 * w, s = kw0 + c;
     const int jb = kw0 / G, sb = jb * G;
@@ -90,10 +90,10 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_kv_kernel(BwdParams p) {
     const float Cs = (suf < pinf()) ? -suf * p.il2 : ninf();  // max a over (s, end of block)
     const float sufpsi = suf - psi_s;
 
-    if constexpr (D < DT) {
-        for (int i = tid; i < (DT - D) * PT; i += NTHREADS) {
-            QT[D * PT + i] = (T)0.f;
-            dOT[D * PT + i] = (T)0.f;
+    if constexpr (D < DT) {  // columns D..31 read by the padded transpose reads stay zero
+        for (int i = tid; i < 2 * TS + (DT - D); i += NTHREADS) {
+            Qs[i] = (T)0.f;
+            dOs[i] = (T)0.f;
         }
     }
     if (tid < BK) kPHI[tid] = (k0 + tid < p.TP) ? p.state[L.plane(PL_PHI) + rowbase + k0 + tid] : pinf();
@@ -104,115 +104,124 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_kv_kernel(BwdParams p) {
         dkacc[dt] = zero16();
         dvacc[dt] = zero16();
     }
-    float gsum = 0.f, dbacc = 0.f, Wacc = 0.f, wblk = 0.f;
+    float gsum = 0.f, dbacc = 0.f, Wacc = 0.f;
     float mid = pinf(), midl = ninf(), cmid = ninf();  // over blocks strictly between jb and ib
-    float rs = ninf(), sv = 0.f;
-    int cur_ib = -1;
-    const float *phiblk = kPHI + (sb - k0);  // phi of this wave's key block (64 values)
+    const float *phiblk = kPHI + (sb - k0);
 
-    for (int q0 = k0; q0 < p.T; q0 += BQ) {
-        const int ib = q0 / G;
-        if (ib != cur_ib) {
-            if (cur_ib > jb) {  // close the previous query block: W and middle-block sums
-                if (rs > ninf()) Wacc += fexp2(Cs - rs) * wblk;
-                if (cur_ib > jb + 1) {
-                    const float tp = wave_sum((rs > ninf()) ? fexp2(cmid - rs) * wblk : 0.f);
-                    if (lane == 0 && wave_active)
-                        p.tbuf[((brow + cur_ib) * p.NB + jb) * 2 + (w & 1)] = tp;
-                }
-                const float bm = p.state[L.bplane(BP_MIN) + brow + cur_ib];
-                mid = fminf(mid, bm);
-                midl = lse2_pair(midl, p.state[L.bplane(BP_LSE) + brow + cur_ib]);
-                cmid = fmaxf(cmid, -bm * p.il2);
-            }
-            wblk = 0.f;
-            cur_ib = ib;
+    TileRegs<T, D, BQ> qr, dor;
+    float pf_lse = 0.f, pf_del = 0.f, pf_pre = 0.f, pf_prel = 0.f;
+    auto gload = [&](int ib) {
+        qr.load(Qb, p.sq.t, ib * BQ, p.T);
+        dor.load(DOb, p.sdo.t, ib * BQ, p.T);
+        if (tid < BQ) {
+            const int64_t r = rowbase + ib * BQ + tid;
+            pf_lse = p.lse[r];
+            pf_del = p.delta[r];
+            pf_pre = p.state[L.plane(PL_PRE) + r];
+            pf_prel = p.state[L.plane(PL_PREL) + r];
+        }
+    };
+    auto lstore = [&](int buf) {
+        qr.store(Qs + buf * TS, PQ);
+        dor.store(dOs + buf * TS, PQ);
+        if (tid < BQ) {
+            rLSE[buf][tid] = pf_lse;
+            rDEL[buf][tid] = pf_del;
+            rPRE[buf][tid] = pf_pre;
+            rPREL[buf][tid] = pf_prel;
+        }
+    };
+
+    const int ib0 = k0 / G;
+    gload(ib0);
+    lstore(0);
+    __syncthreads();
+    for (int ib = ib0, it = 0; ib < p.NB; ++ib, ++it) {
+        const int buf = it & 1;
+        if (ib + 1 < p.NB) gload(ib + 1);
+        if (wave_active && ib >= jb) {
+            float rs = ninf(), sv = 0.f;
             if (ib > jb) {
+                if (ib - 1 > jb) {  // block ib - 1 joins the middle
+                    const float bm = p.state[L.bplane(BP_MIN) + brow + ib - 1];
+                    mid = fminf(mid, bm);
+                    midl = lse2_pair(midl, p.state[L.bplane(BP_LSE) + brow + ib - 1]);
+                    cmid = fmaxf(cmid, -bm * p.il2);
+                }
                 rs = fmaxf(Cs, cmid);
                 sv = (rs > ninf()) ? fexp2(sufl - rs) + fexp2(midl - rs) : 0.f;
             }
-        }
-
-        __syncthreads();
-        stage_rows<T, D, BQ, PQ>(Qs, Qb, p.sq.t, q0, p.T);
-        stage_rows<T, D, BQ, PQ>(dOs, DOb, p.sdo.t, q0, p.T);
-        stage_rows_t<T, D, BQ, PT>(QT, Qb, p.sq.t, q0, p.T);
-        stage_rows_t<T, D, BQ, PT>(dOT, DOb, p.sdo.t, q0, p.T);
-        if (tid < BQ) {
-            rLSE[tid] = p.lse[rowbase + q0 + tid];
-            rDEL[tid] = p.delta[rowbase + q0 + tid];
-            rPRE[tid] = p.state[L.plane(PL_PRE) + rowbase + q0 + tid];
-            rPREL[tid] = p.state[L.plane(PL_PREL) + rowbase + q0 + tid];
-        }
-        __syncthreads();
-        if (!wave_active || q0 + BQ - 1 < kw0) continue;
-
-        f32x16 S = mma_p1_lds_reg<T, D>(zero16(), Qs + c * PQ, g, kreg);   // [t][s]
-        f32x16 dP = mma_p1_lds_reg<T, D>(zero16(), dOs + c * PQ, g, vreg);
-
-        const bool diag = (ib == jb);
-        float Xd[16];
-        if (diag) {
-            // X_ts = min phi(s, t] inside the block: ascending scan from s+1.
-            const int sr = s - sb, qh = (q0 - sb) >> 5;
+            const T *Qt = Qs + buf * TS;
+            const T *Dt = dOs + buf * TS;
+            const bool diag = (ib == jb);
+            const int sr = s - sb;
+            float r = pinf();  // running min of phi over (s, u] for the in-block scan
+            float wblk = 0.f;
+#pragma unroll 1
+            for (int mt = 0; mt < 2; ++mt) {
+                f32x16 S[1], dP[1];
+                S[0] = mma_p1_lds_reg<T, D>(zero16(), Qt + (32 * mt + c) * PQ, g, kreg);   // [t][s]
+                dP[0] = mma_p1_lds_reg<T, D>(zero16(), Dt + (32 * mt + c) * PQ, g, vreg);
+                float X[16];
+                if (diag) {
+                    // X_ts = min phi(s, t] inside the block: ascending scan from s + 1.
 #pragma unroll
-            for (int j = 0; j < 16; ++j) Xd[j] = pinf();
-            float r = pinf();
+                    for (int j = 0; j < 16; ++j) X[j] = pinf();
 #pragma unroll
-            for (int u = 0; u < G; ++u) {
-                r = (u > sr) ? fminf(r, phiblk[u]) : r;
-                const int jj = u & 31, gg = (jj >> 2) & 1, j = (jj >> 3) * 4 + (jj & 3);
-                if ((u >> 5) == qh && gg == g) Xd[j] = r;
+                    for (int uu = 0; uu < 32; ++uu) {
+                        const int u = 32 * mt + uu;
+                        r = (u > sr) ? fminf(r, phiblk[u]) : r;
+                        const int gg = (uu >> 2) & 1, j = (uu >> 3) * 4 + (uu & 3);
+                        if (gg == g) X[j] = r;
+                    }
+                }
+#pragma unroll
+                for (int jq = 0; jq < 4; ++jq) {
+                    const int t4 = 32 * mt + 8 * jq + 4 * g;
+                    const f32x4 lse4 = *reinterpret_cast<const f32x4 *>(&rLSE[buf][t4]);
+                    const f32x4 del4 = *reinterpret_cast<const f32x4 *>(&rDEL[buf][t4]);
+                    const f32x4 pre4 = *reinterpret_cast<const f32x4 *>(&rPRE[buf][t4]);
+                    const f32x4 prl4 = *reinterpret_cast<const f32x4 *>(&rPREL[buf][t4]);
+                    f32x4 g4;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int j = 4 * jq + e;
+                        const int t = ib * BQ + t4 + e;
+                        const bool valid = (t < p.T) && (t >= s) && s_valid;
+                        const bool strict = valid && (t > s);
+                        const float x = diag ? X[j] - psi_s : fminf(sufpsi, fminf(pre4[e], mid) - psi_s);
+                        const float xm = strict ? fminf(x, 0.f) : 0.f;
+                        const float z = fmaf(S[0][j], p.sc2, fmaf(betal, xm, -lse4[e]));
+                        const float P = valid ? fexp2(z) : 0.f;
+                        const float dS = P * (dP[0][j] - del4[e]);
+                        const float gg = (strict && x <= 0.f) ? dS : 0.f;
+                        gsum += gg;
+                        dbacc = fmaf(dS, xm, dbacc);
+                        if (!diag && rs > ninf()) wblk = fmaf(gg, frcp(sv + fexp2(prl4[e] - rs)), wblk);
+                        g4[e] = gg;
+                        S[0][j] = P;
+                        dP[0][j] = dS;
+                    }
+                    if (diag && s_valid)
+                        *reinterpret_cast<f32x4 *>(p.gd + ((brow + jb) * G + sr) * G + t4) = g4;
+                }
+                // dV^T[d][s] += dO^T[d][t] P[t][s];  dK^T[d][s] += Q^T[d][t] dS[t][s]
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) {
+                    dvacc[dt] = mma_p2_p3<T, 1, true>(dvacc[dt], S, Dt + 32 * mt * PQ, PQ, 32 * dt, lane);
+                    dkacc[dt] = mma_p2_p3<T, 1, true>(dkacc[dt], dP, Qt + 32 * mt * PQ, PQ, 32 * dt, lane);
+                }
+            }
+            if (ib > jb) {  // close query block ib: key-block and middle-block soft-min sums
+                if (rs > ninf()) Wacc = fmaf(fexp2(Cs - rs), wblk, Wacc);
+                if (ib > jb + 1) {
+                    const float tp = wave_sum((rs > ninf()) ? fexp2(cmid - rs) * wblk : 0.f);
+                    if (lane == 0) p.tbuf[((brow + ib) * p.NB + jb) * 2 + (w & 1)] = tp;
+                }
             }
         }
-        const float Y0 = mid;
-        float tile_g[16];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const int tr = acc_row(j, g), t = q0 + tr;
-            const bool valid = (t < p.T) && (t >= s) && s_valid;
-            const bool strict = valid && (t > s);
-            float x;
-            if (diag)
-                x = Xd[j] - psi_s;
-            else
-                x = fminf(sufpsi, fminf(rPRE[tr], Y0) - psi_s);
-            const float xm = strict ? fminf(x, 0.f) : 0.f;
-            const float z = S[j] * p.sc2 + betal * xm - rLSE[tr];
-            const float P = valid ? fexp2(z) : 0.f;
-            const float dS = P * (dP[j] - rDEL[tr]);
-            const float gg = (strict && x <= 0.f) ? dS : 0.f;
-            gsum += gg;
-            dbacc += dS * xm;
-            if (!diag && rs > ninf()) wblk += gg * frcp(sv + fexp2(rPREL[tr] - rs));
-            tile_g[j] = gg;
-            S[j] = P;
-            dP[j] = dS;
-        }
-        if (diag && s_valid) {
-            float *gdrow = p.gd + ((brow + jb) * G + (s - sb)) * G + (q0 - sb);
-#pragma unroll
-            for (int jq = 0; jq < 4; ++jq) {
-                f32x4 v4 = {tile_g[4 * jq + 0], tile_g[4 * jq + 1], tile_g[4 * jq + 2], tile_g[4 * jq + 3]};
-                *reinterpret_cast<f32x4 *>(gdrow + 8 * jq + 4 * g) = v4;
-            }
-        }
-
-        // dV^T[d][s] += dO^T[d][t] P[t][s];  dK^T[d][s] += Q^T[d][t] dS[t][s]
-        const f32x16 Pt[1] = {S};
-        const f32x16 dSt[1] = {dP};
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-            dvacc[dt] = mma_p2_p3<T, 1, true>(dvacc[dt], Pt, dOT + (32 * dt + c) * PT, g);
-            dkacc[dt] = mma_p2_p3<T, 1, true>(dkacc[dt], dSt, QT + (32 * dt + c) * PT, g);
-        }
-    }
-    if (cur_ib > jb) {
-        if (rs > ninf()) Wacc += fexp2(Cs - rs) * wblk;
-        if (cur_ib > jb + 1) {
-            const float tp = wave_sum((rs > ninf()) ? fexp2(cmid - rs) * wblk : 0.f);
-            if (lane == 0 && wave_active) p.tbuf[((brow + cur_ib) * p.NB + jb) * 2 + (w & 1)] = tp;
-        }
+        if (ib + 1 < p.NB) lstore(buf ^ 1);
+        __syncthreads();
     }
 
     // Per-key outputs (lanes c and c + 32 hold the same key, different queries).
@@ -259,7 +268,8 @@ static hipError_t launch_prep_t(const BwdParams &p, hipStream_t s) {
 
 template <typename T, int D>
 static hipError_t launch_kv_t(const BwdParams &p, hipStream_t s) {
-    hipLaunchKernelGGL((fpa_bwd_kv_kernel<T, D>), dim3(p.NKV, p.BH), dim3(NTHREADS), 0, s, p);
+    constexpr int WPE = (D >= 128 || (sizeof(T) == 4 && D >= 64)) ? 1 : 2;
+    hipLaunchKernelGGL((fpa_bwd_kv_kernel<T, D, WPE>), dim3(p.NKV, p.BH), dim3(NTHREADS), 0, s, p);
     return hipGetLastError();
 }
 

@@ -2,10 +2,11 @@
 //
 // Reference behaviour: _bwd_q (kernel.py:286-340) of yliu-fort/first-passage-attention.
 // gfx950 design: a workgroup of 4 waves owns 128 queries (one query per lane column)
-// and streams 32-key tiles from the diagonal down to key 0 through LDS (K row-major
-// and transposed, V row-major).  Each wave recomputes S^T = K Q^T and dP^T = V dO^T
-// with Q, dO in registers, accumulates dQ^T += K^T dS^T on the 32x32 MFMA, and
-// reduces per query the query-block soft-min sum
+// and streams 64-key blocks from the diagonal down to key 0 through double-buffered
+// LDS (register prefetch of the next block, one barrier per block).  Each wave
+// recomputes S^T = K Q^T and dP^T = V dO^T with Q, dO in registers, accumulates
+// dQ^T += K^T dS^T on the 32x32 MFMA (K^T read from the row-major tile with LDS
+// transpose reads), and reduces per query the query-block soft-min sum
 //   R_t = sum_{s outside blk(t)} g_ts 2^{c_t} / Z_ts,   c_t = max a over [start of blk(t), t].
 // The diagonal block (keys and query in one 64-block) uses the in-block range minimum.
 #include "fpa_common.h"
@@ -13,18 +14,17 @@
 
 namespace fpa {
 
-template <typename T, int D>
-__global__ void __launch_bounds__(NTHREADS) fpa_bwd_q_kernel(BwdParams p) {
-    constexpr int BM = 128, BK = 32;
+template <typename T, int D, int WPE>
+__global__ void __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+fpa_bwd_q_kernel(BwdParams p) {
+    constexpr int BM = 128, BK = 64;  // queries per workgroup, keys per iteration (one block)
     constexpr int DT = D < 32 ? 32 : D;
     constexpr int NDT = DT / 32;
     constexpr int PK = D + (sizeof(T) == 2 ? 8 : 4);
-    constexpr int PT = BK + 4;
-    __shared__ __attribute__((aligned(16))) T Ks[BK * PK];
-    __shared__ __attribute__((aligned(16))) T Vs[BK * PK];
-    __shared__ __attribute__((aligned(16))) T KT[DT * PT];
-    __shared__ float kSUF[BK], kSUFL[BK], kPSI[BK];
-    __shared__ float bPHI[G];
+    constexpr int TS = BK * PK;
+    __shared__ __attribute__((aligned(16))) T Ks[2 * TS + (DT - D)];
+    __shared__ __attribute__((aligned(16))) T Vs[2 * TS];
+    __shared__ __attribute__((aligned(16))) float kSP[2][BK], kPSI[2][BK], kSUFL[2][BK], kPHI[2][BK];
 
     const int tid = threadIdx.x, w = tid / 64, lane = tid % 64, g = lane / 32, c = lane % 32;
     const int qt = gridDim.x - 1 - blockIdx.x;  // longest rows first
@@ -58,7 +58,7 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_q_kernel(BwdParams p) {
     const float prel_ct = fexp2(prel - ct);
 
     if constexpr (D < DT) {
-        for (int i = tid; i < (DT - D) * PT; i += NTHREADS) KT[D * PT + i] = (T)0.f;
+        for (int i = tid; i < 2 * TS + (DT - D); i += NTHREADS) Ks[i] = (T)0.f;
     }
 
     f32x16 dqacc[NDT];
@@ -66,79 +66,101 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_q_kernel(BwdParams p) {
     for (int dt = 0; dt < NDT; ++dt) dqacc[dt] = zero16();
     float racc = 0.f;
     float mid = pinf(), midl = ninf();  // over blocks strictly between jb and ib
-    float mterm = prel_ct;
-    int cur_jb = -1;
 
-    const int nk = (p.T + BK - 1) / BK;
-    const int ktmax = min(nk - 1, (q0 + BM - 1) / BK);
-    for (int kt = ktmax; kt >= 0; --kt) {
-        const int k0 = kt * BK;
-        const int jb = k0 / G;
-        if (jb != cur_jb) {
-            // Entering key block jb from jb + 1: block jb + 1 joins the middle if it lies below ib.
-            if (cur_jb >= 0 && cur_jb < ib) {
-                mid = fminf(mid, p.state[L.bplane(BP_MIN) + brow + cur_jb]);
-                midl = lse2_pair(midl, p.state[L.bplane(BP_LSE) + brow + cur_jb]);
-            }
-            cur_jb = jb;
-            mterm = fexp2(midl - ct) + prel_ct;
-        }
-        __syncthreads();
-        stage_rows<T, D, BK, PK>(Ks, Kb, p.sk.t, k0, p.T);
-        stage_rows<T, D, BK, PK>(Vs, Vb, p.sv.t, k0, p.T);
-        stage_rows_t<T, D, BK, PT>(KT, Kb, p.sk.t, k0, p.T);
+    TileRegs<T, D, BK> kr, vr;
+    float pf_suf = 0.f, pf_psi = 0.f, pf_sufl = 0.f, pf_phi = 0.f;
+    auto gload = [&](int jb) {
+        kr.load(Kb, p.sk.t, jb * BK, p.T);
+        vr.load(Vb, p.sv.t, jb * BK, p.T);
         if (tid < BK) {
-            kSUF[tid] = p.state[L.plane(PL_SUF) + rowbase + k0 + tid];
-            kSUFL[tid] = p.state[L.plane(PL_SUFL) + rowbase + k0 + tid];
-            kPSI[tid] = p.state[L.plane(PL_PSI) + rowbase + k0 + tid];
-        } else if (tid >= 64 && tid < 64 + G) {
-            bPHI[tid - 64] = p.state[L.plane(PL_PHI) + rowbase + jb * G + (tid - 64)];
+            const int64_t r = rowbase + jb * BK + tid;
+            pf_suf = p.state[L.plane(PL_SUF) + r];
+            pf_psi = p.state[L.plane(PL_PSI) + r];
+            pf_sufl = p.state[L.plane(PL_SUFL) + r];
+            pf_phi = p.state[L.plane(PL_PHI) + r];
         }
-        __syncthreads();
-        if (!wave_active || k0 > qw0 + 31) continue;
+    };
+    auto lstore = [&](int buf) {
+        kr.store(Ks + buf * TS, PK);
+        vr.store(Vs + buf * TS, PK);
+        if (tid < BK) {
+            kSP[buf][tid] = pf_suf - pf_psi;
+            kPSI[buf][tid] = pf_psi;
+            kSUFL[buf][tid] = pf_sufl;
+            kPHI[buf][tid] = pf_phi;
+        }
+    };
 
-        f32x16 S = mma_p1_lds_reg<T, D>(zero16(), Ks + c * PK, g, qreg);    // [s][t]
-        f32x16 dP = mma_p1_lds_reg<T, D>(zero16(), Vs + c * PK, g, doreg);
-
-        const bool diag = (jb == ib);
-        float Xd[16];
-        if (diag) {
-            // X_ts = min phi(s, t] inside the block: descending scan down to s+1.
-            const int tr = tq - jb * G, kh = (k0 - jb * G) >> 5;
+    const int jbmax = min(p.NB - 1, (q0 + BM - 1) / BK);
+    gload(jbmax);
+    lstore(0);
+    __syncthreads();
+    for (int jb = jbmax, it = 0; jb >= 0; --jb, ++it) {
+        const int buf = it & 1;
+        const int s0 = jb * BK;
+        if (jb > 0) gload(jb - 1);
+        if (wave_active && jb <= ib) {
+            if (jb + 1 < ib) {  // block jb + 1 joins the middle
+                mid = fminf(mid, p.state[L.bplane(BP_MIN) + brow + jb + 1]);
+                midl = lse2_pair(midl, p.state[L.bplane(BP_LSE) + brow + jb + 1]);
+            }
+            const float mterm = fexp2(midl - ct) + prel_ct;
+            const float Y = fminf(pre, mid);
+            const bool diag = (jb == ib);
+            const int tr = tq - s0;
+            const T *Kt = Ks + buf * TS;
+            const T *Vt = Vs + buf * TS;
+            float r = pinf();  // running min of phi over [u, t] for the in-block scan
+#pragma unroll 1
+            for (int mt = 1; mt >= 0; --mt) {
+                f32x16 S[1], dP[1];
+                S[0] = mma_p1_lds_reg<T, D>(zero16(), Kt + (32 * mt + c) * PK, g, qreg);   // [s][t]
+                dP[0] = mma_p1_lds_reg<T, D>(zero16(), Vt + (32 * mt + c) * PK, g, doreg);
+                float X[16];
+                if (diag) {
+                    // X_ts = min phi(s, t] inside the block: descending scan down to s + 1.
 #pragma unroll
-            for (int j = 0; j < 16; ++j) Xd[j] = pinf();
-            float r = pinf();
+                    for (int j = 0; j < 16; ++j) X[j] = pinf();
 #pragma unroll
-            for (int u = G - 1; u >= 1; --u) {
-                r = (u <= tr) ? fminf(r, bPHI[u]) : r;
-                const int sr = u - 1, jj = sr & 31, gg = (jj >> 2) & 1, j = (jj >> 3) * 4 + (jj & 3);
-                if ((sr >> 5) == kh && gg == g) Xd[j] = r;
+                    for (int uu = 32; uu >= 1; --uu) {
+                        const int u = 32 * mt + uu;  // key u - 1 gets min phi[u .. t]
+                        if (u < G) r = (u <= tr) ? fminf(r, kPHI[buf][u]) : r;
+                        const int sr = uu - 1, gg = (sr >> 2) & 1, j = (sr >> 3) * 4 + (sr & 3);
+                        if (gg == g) X[j] = r;
+                    }
+                }
+#pragma unroll
+                for (int jq = 0; jq < 4; ++jq) {
+                    const int s4 = 32 * mt + 8 * jq + 4 * g;
+                    const f32x4 sp4 = *reinterpret_cast<const f32x4 *>(&kSP[buf][s4]);
+                    const f32x4 psi4 = *reinterpret_cast<const f32x4 *>(&kPSI[buf][s4]);
+                    const f32x4 sfl4 = *reinterpret_cast<const f32x4 *>(&kSUFL[buf][s4]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int j = 4 * jq + e;
+                        const int s = s0 + s4 + e;
+                        const bool valid = t_valid && (s <= tq);
+                        const bool strict = valid && (s < tq);
+                        const float x = diag ? X[j] - psi4[e] : fminf(sp4[e], Y - psi4[e]);
+                        const float xm = strict ? fminf(x, 0.f) : 0.f;
+                        const float z = fmaf(S[0][j], p.sc2, fmaf(betal, xm, -lse));
+                        const float P = valid ? fexp2(z) : 0.f;
+                        const float dS = P * (dP[0][j] - del);
+                        if (!diag) {
+                            const float gg = (strict && x <= 0.f) ? dS : 0.f;
+                            racc = fmaf(gg, frcp(fexp2(sfl4[e] - ct) + mterm), racc);
+                        }
+                        S[0][j] = dS;
+                    }
+                }
+                // dQ^T[d][t] += K^T[d][s] dS^T[s][t]   (K read transposed from its natural layout)
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt)
+                    dqacc[dt] = mma_p2_p3<T, 1, true>(dqacc[dt], S, Kt + 32 * mt * PK, PK, 32 * dt, lane);
             }
         }
-        const float Y = fminf(pre, mid);
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const int sr = acc_row(j, g), s = k0 + sr;
-            const bool valid = t_valid && (s <= tq);
-            const bool strict = valid && (s < tq);
-            const float psi_s = kPSI[sr];
-            float x;
-            if (diag)
-                x = Xd[j] - psi_s;
-            else
-                x = fminf(kSUF[sr] - psi_s, Y - psi_s);
-            const float xm = strict ? fminf(x, 0.f) : 0.f;
-            const float z = S[j] * p.sc2 + betal * xm - lse;
-            const float P = valid ? fexp2(z) : 0.f;
-            const float dS = P * (dP[j] - del);
-            const float gg = (strict && x <= 0.f) ? dS : 0.f;
-            if (!diag) racc += gg * frcp(fexp2(kSUFL[sr] - ct) + mterm);
-            S[j] = dS;
-        }
-        // dQ^T[d][t] += K^T[d][s] dS^T[s][t]
-        const f32x16 dSt[1] = {S};
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) dqacc[dt] = mma_p2_p3<T, 1, true>(dqacc[dt], dSt, KT + (32 * dt + c) * PT, g);
+        if (jb > 0) lstore(buf ^ 1);
+        __syncthreads();
     }
 
     racc += __shfl_xor(racc, 32, 64);
@@ -168,7 +190,8 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_q_kernel(BwdParams p) {
 template <typename T, int D>
 static hipError_t launch_q_t(const BwdParams &p, hipStream_t s) {
     const int nqt = (p.T + 127) / 128;
-    hipLaunchKernelGGL((fpa_bwd_q_kernel<T, D>), dim3(nqt, p.BH), dim3(NTHREADS), 0, s, p);
+    constexpr int WPE = (D >= 128 && sizeof(T) == 4) ? 1 : 2;
+    hipLaunchKernelGGL((fpa_bwd_q_kernel<T, D, WPE>), dim3(nqt, p.BH), dim3(NTHREADS), 0, s, p);
     return hipGetLastError();
 }
 

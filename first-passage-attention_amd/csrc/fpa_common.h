@@ -55,6 +55,9 @@ __device__ __forceinline__ float lse2_pair(float a, float b) {
     return m + flog2(1.0f + fexp2(d));
 }
 
+// Element (row, column) of accumulator register j for lane group g (column = lane % 32).
+__device__ __forceinline__ constexpr int acc_row(int j, int g) { return 8 * (j / 4) + 4 * g + (j % 4); }
+
 __device__ __forceinline__ f32x16 zero16() {
     f32x16 z;
 #pragma unroll
@@ -91,36 +94,6 @@ template <typename T, int K> struct P1Count {
 };
 // Register array of the P1 operands of one row.
 template <typename T, int K> using OpRow = typename MT<T>::op_t[P1Count<T, K>::N];
-
-// P1 operand `i` for contraction length K from a row-major source row (LDS or global).
-template <typename T, int K>
-__device__ __forceinline__ typename MT<T>::op_t p1_load(const T *row, int g, int i);
-
-template <>
-__device__ __forceinline__ h8 p1_load<f16, 16>(const f16 *row, int g, int i) {
-    return *reinterpret_cast<const h8 *>(row + 16 * i + 8 * g);
-}
-#define FPA_P1_F16(K)                                                                 \
-    template <>                                                                       \
-    __device__ __forceinline__ h8 p1_load<f16, K>(const f16 *row, int g, int i) {     \
-        return *reinterpret_cast<const h8 *>(row + 16 * i + 8 * g);                   \
-    }
-FPA_P1_F16(32)
-FPA_P1_F16(64)
-FPA_P1_F16(128)
-FPA_P1_F16(256)
-#undef FPA_P1_F16
-#define FPA_P1_F32(K)                                                                 \
-    template <>                                                                       \
-    __device__ __forceinline__ float p1_load<float, K>(const float *row, int g, int i) { \
-        return row[g * (K / 2) + i];                                                  \
-    }
-FPA_P1_F32(16)
-FPA_P1_F32(32)
-FPA_P1_F32(64)
-FPA_P1_F32(128)
-FPA_P1_F32(256)
-#undef FPA_P1_F32
 
 // All P1 operands of one row, read with 16-byte loads (row must be 16-byte aligned).
 template <typename T, int K>
@@ -175,12 +148,40 @@ __device__ __forceinline__ f32x16 mma_p1_lds_reg(f32x16 acc, const T *arow, int 
     return acc;
 }
 
-// acc += A * B where A (or B) comes from accumulator tiles c[0..NT) (P2) and the partner from
-// the transposed LDS row xt[krow] (P3).  `a_is_p3` selects which operand slot the P3 value takes:
-// true -> P3 is the A operand (rows of the product indexed by the transposed source's n);
-// false -> P3 is the B operand.
+// ---------------------------------------------------------------------------
+// P3 operands read from a natural-layout LDS tile X[krow][n] (pitch in elements).
+//
+// fp16: ds_read_b64_tr_b16.  Within each group of 16 lanes, input lane j supplies the
+// four 16-bit elements a_j[0..3] at its address and output lane i receives
+// b_i[k] = a_{4k + i/4}[i % 4].  Pointing input lane j at X[R + j/4][n0 + 4*(j%4)]
+// therefore hands output lane i the column n0 + i of rows R..R+3.
+// ---------------------------------------------------------------------------
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+__device__ __forceinline__ h4 ds_read_tr16(const f16 *p) {
+    const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(p));
+    return __builtin_bit_cast(h4, v);
+}
+
+// fp16 P3 operand of contraction rows rbase + 4g + {0..3, 8..11} at column ncol0 + c.
+__device__ __forceinline__ h8 p3_tr(const f16 *X, int pitch, int rbase, int ncol0, int lane) {
+    const int j = lane & 15, q = lane >> 4;
+    const int row = rbase + 4 * (q >> 1) + (j >> 2);
+    const int col = ncol0 + 16 * (q & 1) + 4 * (j & 3);
+    const f16 *p0 = X + row * pitch + col;
+    const h4 lo = ds_read_tr16(p0);
+    const h4 hi = ds_read_tr16(p0 + 8 * pitch);
+    return h8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// acc += A * B where one operand comes from accumulator tiles c[0..NT) (P2, their rows being
+// the contraction index) and the other from the natural-layout LDS tile X[krow][n] at
+// column n = ncol0 + lane % 32 (P3).  A_IS_P3: the P3 value is the A operand.
 template <typename T, int NT, bool A_IS_P3>
-__device__ __forceinline__ f32x16 mma_p2_p3(f32x16 acc, const f32x16 (&c)[NT], const T *xt, int g) {
+__device__ __forceinline__ f32x16 mma_p2_p3(f32x16 acc, const f32x16 (&c)[NT], const T *X, int pitch, int ncol0,
+                                            int lane) {
+    const int g = lane >> 5;
     if constexpr (sizeof(T) == 2) {
 #pragma unroll
         for (int mt = 0; mt < NT; ++mt) {
@@ -189,24 +190,18 @@ __device__ __forceinline__ f32x16 mma_p2_p3(f32x16 acc, const f32x16 (&c)[NT], c
                 h8 p2;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) p2[e] = (f16)c[mt][8 * hf + e];
-                const int R = 32 * mt + 16 * hf + 4 * g;
-                h4 lo = *reinterpret_cast<const h4 *>(xt + R);
-                h4 hi = *reinterpret_cast<const h4 *>(xt + R + 8);
-                h8 p3 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                const h8 p3 = p3_tr(X, pitch, 32 * mt + 16 * hf, ncol0, lane);
                 acc = A_IS_P3 ? MT<T>::mma(p3, p2, acc) : MT<T>::mma(p2, p3, acc);
             }
         }
     } else {
+        const int n = ncol0 + (lane & 31);
 #pragma unroll
         for (int mt = 0; mt < NT; ++mt) {
 #pragma unroll
-            for (int jq = 0; jq < 4; ++jq) {
-                f32x4 p3 = *reinterpret_cast<const f32x4 *>(xt + 32 * mt + 8 * jq + 4 * g);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float p2 = c[mt][4 * jq + e];
-                    acc = A_IS_P3 ? MT<T>::mma(p3[e], p2, acc) : MT<T>::mma(p2, p3[e], acc);
-                }
+            for (int j = 0; j < 16; ++j) {
+                const float p3 = X[(32 * mt + acc_row(j, g)) * pitch + n];
+                acc = A_IS_P3 ? MT<T>::mma(p3, c[mt][j], acc) : MT<T>::mma(c[mt][j], p3, acc);
             }
         }
     }
@@ -214,61 +209,35 @@ __device__ __forceinline__ f32x16 mma_p2_p3(f32x16 acc, const f32x16 (&c)[NT], c
 }
 
 // ---------------------------------------------------------------------------
-// Global -> LDS staging.  Rows r in [0, NR) of a (B, H, T, D)-strided tensor at
-// positions row0 + r; rows at or past T are zero-filled.
+// Register prefetch of an NR x D tile of a (B, H, T, D)-strided tensor (rows row0 + r,
+// zero past T), stored afterwards into a natural-layout LDS tile of the given pitch.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int NR, int PITCH>
-__device__ __forceinline__ void stage_rows(T *dst, const T *src, int64_t st, int row0, int T_) {
-    constexpr int CE = MT<T>::CHUNK;
-    constexpr int CPR = (D + CE - 1) / CE;    // chunks per row
-    for (int idx = threadIdx.x; idx < NR * CPR; idx += NTHREADS) {
-        const int r = idx / CPR, cc = idx % CPR;
-        f32x4 v = {0.f, 0.f, 0.f, 0.f};
-        if (row0 + r < T_) v = *reinterpret_cast<const f32x4 *>(src + (int64_t)(row0 + r) * st + cc * CE);
-        *reinterpret_cast<f32x4 *>(dst + r * PITCH + cc * CE) = v;
-    }
-}
-
-// Transposed staging: dst[d][r] = src[row0 + r][d] for d < D, r < NR (rows >= T -> 0).
-template <typename T, int D, int NR, int PITCHT>
-__device__ __forceinline__ void stage_rows_t(T *dst, const T *src, int64_t st, int row0, int T_) {
-    constexpr int CE = MT<T>::CHUNK;
-    constexpr int CPR = (D + CE - 1) / CE;
-    constexpr int UNITS = (NR / 4) * CPR;     // 4 rows x one chunk per unit
-    for (int idx = threadIdx.x; idx < UNITS; idx += NTHREADS) {
-        const int r4 = idx / CPR, cc = idx % CPR;
-        const int r = 4 * r4;
-        if constexpr (sizeof(T) == 2) {
-            h8 v[4];
+template <typename T, int D, int NR> struct TileRegs {
+    static constexpr int CE = MT<T>::CHUNK;
+    static constexpr int CPR = D / CE;
+    static constexpr int NCH = NR * CPR;
+    static constexpr int PER = (NCH + NTHREADS - 1) / NTHREADS;
+    f32x4 r[PER];
+    __device__ __forceinline__ void load(const T *base, int64_t st, int row0, int T_) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if (row0 + r + i < T_)
-                    v[i] = *reinterpret_cast<const h8 *>(src + (int64_t)(row0 + r + i) * st + cc * CE);
-                else
-                    v[i] = h8{0, 0, 0, 0, 0, 0, 0, 0};
-            }
-#pragma unroll
-            for (int e = 0; e < CE; ++e) {
-                h4 w = {v[0][e], v[1][e], v[2][e], v[3][e]};
-                *reinterpret_cast<h4 *>(dst + (cc * CE + e) * PITCHT + r) = w;
-            }
-        } else {
-            f32x4 v[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                if (row0 + r + i < T_)
-                    v[i] = *reinterpret_cast<const f32x4 *>(src + (int64_t)(row0 + r + i) * st + cc * CE);
-                else
-                    v[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-            }
-#pragma unroll
-            for (int e = 0; e < CE; ++e) {
-                f32x4 w = {v[0][e], v[1][e], v[2][e], v[3][e]};
-                *reinterpret_cast<f32x4 *>(dst + (cc * CE + e) * PITCHT + r) = w;
-            }
+        for (int i = 0; i < PER; ++i) {
+            const int idx = threadIdx.x + i * NTHREADS;
+            const int row = idx / CPR, cc = idx % CPR;
+            f32x4 v = {0.f, 0.f, 0.f, 0.f};
+            if (idx < NCH && row0 + row < T_)
+                v = *reinterpret_cast<const f32x4 *>(base + (int64_t)(row0 + row) * st + cc * CE);
+            r[i] = v;
         }
     }
-}
+    __device__ __forceinline__ void store(T *dst, int pitch) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int idx = threadIdx.x + i * NTHREADS;
+            const int row = idx / CPR, cc = idx % CPR;
+            if (idx < NCH) *reinterpret_cast<f32x4 *>(dst + row * pitch + cc * CE) = r[i];
+        }
+    }
+};
 
 // Register P1 operands of one global row (zeros when the row is past T).
 template <typename T, int D>
@@ -286,8 +255,6 @@ __device__ __forceinline__ float wave_sum(float x) {
     return x;
 }
 
-// Element (row, column) of accumulator register j for lane group g (column = lane % 32).
-__device__ __forceinline__ constexpr int acc_row(int j, int g) { return 8 * (j / 4) + 4 * g + (j % 4); }
 
 // State planes (float offsets), each plane is BH * TP floats except the two block planes.
 struct StateLayout {

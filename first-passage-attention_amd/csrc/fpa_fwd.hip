@@ -5,9 +5,11 @@
 //   * statistics: one wave per block of G = 64 positions, prefix/suffix min and
 //     base-2 log-sum-exp by wave shuffles;
 //   * forward: a workgroup of 4 waves owns 128 query rows (32 per wave), streams
-//     64-key tiles from the diagonal down to key 0 through LDS (K row-major, V
-//     transposed), computes S^T = K Q^T and O^T += V^T P^T on the 32x32 MFMA, and
-//     keeps each query's online-softmax state in its own lane.
+//     64-key tiles from the diagonal down to key 0 through double-buffered LDS
+//     (register prefetch of the next tile, one barrier per tile), computes
+//     S^T = K Q^T and O^T += V^T P^T on the 32x32 MFMA (V^T read from the row-major
+//     tile with LDS transpose reads), and keeps each query's online-softmax state in
+//     its own lane.
 #include "fpa_common.h"
 #include "fpa_params.h"
 
@@ -78,17 +80,30 @@ hipError_t launch_stats(const StatsParams &p, hipStream_t s) {
 
 // ---------------------------------------------------------------------------
 // Forward.
+//
+// Per lane: one query t (column c of the 32x32 accumulators) and, per 64-key tile,
+// 32 of the keys.  Off the diagonal block the bias is built from three per-key values
+// staged in LDS and one per-query value in a register:
+//   b2 = med3(A_s, Y_t - P_s, E),  A_s = beta*log2e*min(SUF_s - psi_s, 0),
+//   P_s = beta*log2e*psi_s, Y_t = beta*log2e*min(PRE_t, MID), E = -inf (beta >= 0) or +inf,
+// which is beta*log2e*min(0, min(SUF_s, MID, PRE_t) - psi_s) for either sign of beta.
+// On the diagonal block X_ts = min phi(s, t] comes from a scan down the block.
+// The running max is only moved when a row's tile max exceeds it by more than 8 (base 2):
+// p <= 256 and the O rescale is skipped on most tiles.
 // ---------------------------------------------------------------------------
-template <typename T, int D>
-__global__ void __launch_bounds__(NTHREADS) fpa_fwd_kernel(FwdParams p) {
+constexpr float RESCALE_SLACK = 8.f;
+
+template <typename T, int D, int WPE>
+__global__ void __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+fpa_fwd_kernel(FwdParams p) {
     constexpr int BM = 128, BN = 64;
     constexpr int DT = D < 32 ? 32 : D;
     constexpr int NDT = DT / 32;
-    constexpr int PK = D + (sizeof(T) == 2 ? 8 : 4);  // K tile pitch (elements)
-    constexpr int PV = BN + 4;                          // V^T tile pitch (elements)
-    __shared__ __attribute__((aligned(16))) T Ks[BN * PK];
-    __shared__ __attribute__((aligned(16))) T VT[DT * PV];
-    __shared__ float sSUF[BN], sPSI[BN], sPHI[BN];
+    constexpr int PK = D + (sizeof(T) == 2 ? 8 : 4);  // tile pitch (elements)
+    constexpr int TS = BN * PK;                          // one tile
+    __shared__ __attribute__((aligned(16))) T Ks[2 * TS];
+    __shared__ __attribute__((aligned(16))) T Vs[2 * TS + (DT - D)];
+    __shared__ __attribute__((aligned(16))) float cA[2][BN], cP[2][BN], cPHI[2][BN];
 
     const int tid = threadIdx.x, w = tid / 64, lane = tid % 64, g = lane / 32, c = lane % 32;
     const int qt = gridDim.x - 1 - blockIdx.x;  // longest rows first
@@ -106,12 +121,9 @@ __global__ void __launch_bounds__(NTHREADS) fpa_fwd_kernel(FwdParams p) {
     OpRow<T, D> qreg;
     load_row_p1<T, D>(qreg, Qb + (int64_t)tq * p.sq.t, tq < p.T, g);
 
-    const float betal = p.beta[h] * LOG2E;
+    const float beta = p.beta[h], betal = beta * LOG2E;
+    const float E = (beta >= 0.f) ? ninf() : pinf();
     const float pre_t = (tq < p.TP) ? p.state[L.plane(PL_PRE) + rowbase + tq] : pinf();
-
-    if constexpr (D < DT) {  // rows D..31 of V^T stay zero
-        for (int i = tid; i < (DT - D) * PV; i += NTHREADS) VT[D * PV + i] = (T)0.f;
-    }
 
     float m_i = ninf(), l_i = 0.f;
     f32x16 oacc[NDT];
@@ -122,99 +134,131 @@ __global__ void __launch_bounds__(NTHREADS) fpa_fwd_kernel(FwdParams p) {
     const int jtmax = min(nkt - 1, (q0 + BM - 1) / BN);
     float mid = pinf();  // min phi over the blocks strictly between the key block and ib
 
-    for (int jt = jtmax; jt >= 0; --jt) {
-        const int s0 = jt * BN;
-        __syncthreads();
-        stage_rows<T, D, BN, PK>(Ks, Kb, p.sk.t, s0, p.T);
-        stage_rows_t<T, D, BN, PV>(VT, Vb, p.sv.t, s0, p.T);
+    TileRegs<T, D, BN> kr, vr;
+    float pf_suf = 0.f, pf_psi = 0.f, pf_phi = 0.f;
+    auto gload = [&](int jt) {
+        kr.load(Kb, p.sk.t, jt * BN, p.T);
+        vr.load(Vb, p.sv.t, jt * BN, p.T);
         if (tid < BN) {
-            sSUF[tid] = p.state[L.plane(PL_SUF) + rowbase + s0 + tid];
-            sPSI[tid] = p.state[L.plane(PL_PSI) + rowbase + s0 + tid];
-            sPHI[tid] = p.state[L.plane(PL_PHI) + rowbase + s0 + tid];
+            const int64_t r = rowbase + jt * BN + tid;
+            pf_suf = p.state[L.plane(PL_SUF) + r];
+            pf_psi = p.state[L.plane(PL_PSI) + r];
+            pf_phi = p.state[L.plane(PL_PHI) + r];
         }
+    };
+    auto lstore = [&](int buf) {
+        kr.store(Ks + buf * TS, PK);
+        vr.store(Vs + buf * TS, PK);
+        if (tid < BN) {
+            cA[buf][tid] = betal * fminf(pf_suf - pf_psi, 0.f);
+            cP[buf][tid] = betal * pf_psi;
+            cPHI[buf][tid] = pf_phi;
+        }
+    };
+    if constexpr (D < DT) {  // V columns D..31 read by the padded transpose reads stay zero
+        for (int i = tid; i < 2 * TS + (DT - D); i += NTHREADS) Vs[i] = (T)0.f;
         __syncthreads();
-        if (!wave_active || s0 > qw0 + 31) continue;
+    }
 
-        f32x16 s[2];
+    gload(jtmax);
+    lstore(0);
+    __syncthreads();
+    for (int jt = jtmax, it = 0; jt >= 0; --jt, ++it) {
+        const int buf = it & 1;
+        const int s0 = jt * BN;
+        if (jt > 0) gload(jt - 1);
+        if (wave_active && s0 <= qw0 + 31) {
+            const T *Kt = Ks + buf * TS;
+            f32x16 s[2];
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) s[mt] = mma_p1_lds_reg<T, D>(zero16(), Ks + (32 * mt + c) * PK, g, qreg);
+            for (int mt = 0; mt < 2; ++mt) s[mt] = mma_p1_lds_reg<T, D>(zero16(), Kt + (32 * mt + c) * PK, g, qreg);
 
-        const int jb = jt;  // BN == G: the key tile is one statistics block
-        if (jb < ib) {
-            const float Y = fminf(pre_t, mid);
+            const int jb = jt;  // BN == G: the key tile is one statistics block
+            if (jb < ib) {
+                const float Y = betal * fminf(pre_t, mid);
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
+                for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    const int sr = 32 * mt + acc_row(j, g);
-                    const float x = fminf(sSUF[sr], Y) - sPSI[sr];
-                    s[mt][j] = s[mt][j] * p.sc2 + betal * fminf(x, 0.f);
+                    for (int jq = 0; jq < 4; ++jq) {
+                        const int s4 = 32 * mt + 8 * jq + 4 * g;
+                        const f32x4 a4 = *reinterpret_cast<const f32x4 *>(&cA[buf][s4]);
+                        const f32x4 p4 = *reinterpret_cast<const f32x4 *>(&cP[buf][s4]);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float b2 = __builtin_amdgcn_fmed3f(a4[e], Y - p4[e], E);
+                            s[mt][4 * jq + e] = fmaf(s[mt][4 * jq + e], p.sc2, b2);
+                        }
+                    }
+            } else {
+                // Diagonal block: X_ts = min phi(s, t] inside the block, by a descending scan.
+                const int tr = tq - s0;
+                float X[2][16];
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) X[mt][j] = pinf();
+                float r = pinf();
+#pragma unroll
+                for (int u = BN - 1; u >= 1; --u) {
+                    r = (u <= tr) ? fminf(r, cPHI[buf][u]) : r;
+                    const int sr = u - 1, mt = sr >> 5, jj = sr & 31;
+                    const int gg = (jj >> 2) & 1, j = (jj >> 3) * 4 + (jj & 3);
+                    if (gg == g) X[mt][j] = r;
                 }
-        } else {
-            // Diagonal block: X_ts = min phi(s, t] inside the block, by a descending scan.
-            const int tr = tq - s0;
-            float X[2][16];
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
+                for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-                for (int j = 0; j < 16; ++j) X[mt][j] = pinf();
-            float r = pinf();
-#pragma unroll
-            for (int u = BN - 1; u >= 1; --u) {
-                const float ph = sPHI[u];
-                r = (u <= tr) ? fminf(r, ph) : r;
-                const int sr = u - 1, mt = sr >> 5, jj = sr & 31;
-                const int gg = (jj >> 2) & 1, j = (jj >> 3) * 4 + (jj & 3);
-                if (gg == g) X[mt][j] = r;
+                    for (int j = 0; j < 16; ++j) {
+                        const int sr = 32 * mt + acc_row(j, g);
+                        float z;
+                        if (sr > tr || s0 + sr >= p.T)
+                            z = ninf();
+                        else if (sr == tr)
+                            z = s[mt][j] * p.sc2;
+                        else
+                            z = fmaf(s[mt][j], p.sc2,
+                                     __builtin_amdgcn_fmed3f(0.f, fmaf(betal, X[mt][j], -cP[buf][sr]), E));
+                        s[mt][j] = z;
+                    }
             }
+
+            // Online softmax (base 2); lanes c and c + 32 hold the same query.
+            float mx = ninf();
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[mt][j]);
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            if (__any(mx > m_i + RESCALE_SLACK)) {
+                const float m_new = fmaxf(m_i, mx);
+                const float alpha = fexp2(m_i - m_new);  // 0 on the first tile (m_i = -inf)
+                l_i *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) oacc[dt][j] *= alpha;
+                m_i = m_new;
+            }
+            float rs = 0.f;
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
                 for (int j = 0; j < 16; ++j) {
-                    const int sr = 32 * mt + acc_row(j, g);
-                    float z;
-                    if (sr > tr || s0 + sr >= p.T)
-                        z = ninf();
-                    else if (sr == tr)
-                        z = s[mt][j] * p.sc2;
-                    else
-                        z = s[mt][j] * p.sc2 + betal * fminf(X[mt][j] - sPSI[sr], 0.f);
-                    s[mt][j] = z;
+                    const float pv = fexp2(s[mt][j] - m_i);
+                    s[mt][j] = pv;
+                    rs += pv;
                 }
+            l_i += rs + __shfl_xor(rs, 32, 64);
+
+            // O^T[d][t] += V^T[d][s] P^T[s][t]   (V read transposed from its natural layout)
+            const T *Vt = Vs + buf * TS;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mma_p2_p3<T, 2, true>(oacc[dt], s, Vt, PK, 32 * dt, lane);
+
+            if (jb < ib) mid = fminf(mid, p.state[L.bplane(BP_MIN) + (int64_t)bh * p.NB + jb]);
         }
-
-        // Online softmax (base 2).  Lanes c and c+32 hold the same query.
-        float mx = ninf();
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[mt][j]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = fmaxf(m_i, mx);
-        const float m_use = (m_new == ninf()) ? 0.f : m_new;
-        const float alpha = fexp2(m_i - m_use);
-        float rs = 0.f;
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const float pv = fexp2(s[mt][j] - m_use);
-                s[mt][j] = pv;
-                rs += pv;
-            }
-        rs += __shfl_xor(rs, 32, 64);
-        l_i = l_i * alpha + rs;
-        m_i = m_new;
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) oacc[dt][j] *= alpha;
-
-        // O^T[d][t] += V^T[d][s] P^T[s][t]
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mma_p2_p3<T, 2, true>(oacc[dt], s, VT + (32 * dt + c) * PV, g);
-
-        if (jb < ib) mid = fminf(mid, p.state[L.bplane(BP_MIN) + (int64_t)bh * p.NB + jb]);
+        if (jt > 0) lstore(buf ^ 1);
+        __syncthreads();
     }
 
     if (!wave_active) return;
@@ -245,7 +289,8 @@ __global__ void __launch_bounds__(NTHREADS) fpa_fwd_kernel(FwdParams p) {
 template <typename T, int D>
 static hipError_t launch_fwd_t(const FwdParams &p, hipStream_t s) {
     const int nqt = (p.T + 127) / 128;
-    hipLaunchKernelGGL((fpa_fwd_kernel<T, D>), dim3(nqt, p.BH), dim3(NTHREADS), 0, s, p);
+    constexpr int WPE = (sizeof(T) == 4 && D >= 128) ? 1 : 2;
+    hipLaunchKernelGGL((fpa_fwd_kernel<T, D, WPE>), dim3(nqt, p.BH), dim3(NTHREADS), 0, s, p);
     return hipGetLastError();
 }
 
