@@ -93,6 +93,9 @@ def main():
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="first run one device-to-device copy of this many MiB (a known-size kernel that "
+                         "calibrates the FETCH_SIZE / WRITE_SIZE counters of a profiling run)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -106,6 +109,12 @@ def main():
     cfg = CONFIGS[a.config]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if a.copy_mib:
+        src = torch.ones(a.copy_mib << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     q, k, v, phi, psi, beta, do = (t.to(dev) for t in make_inputs(cfg))
     leaves = [t.clone().requires_grad_() for t in (q, k, v, phi, psi, beta)]
 

@@ -20,6 +20,9 @@ ARCH = os.environ.get("FPA_OFFLOAD_ARCH", "gfx950")
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-I", os.path.join(ROOT, "include"),
           "-I", CSRC,
+          # No NaN inputs or intermediates are relied on (infinities are): min/max need no
+          # NaN quieting, so IEEE mode is off and fminf/fmaxf map to single instructions.
+          "-fno-honor-nans", "-mno-amdgpu-ieee",
           # Packed fp32 VALU ops stay disabled: unpacked fp32 arithmetic only.
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 

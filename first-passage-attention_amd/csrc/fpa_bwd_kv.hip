@@ -60,9 +60,12 @@ fpa_bwd_kv_kernel(BwdParams p) {
     __shared__ __attribute__((aligned(16))) float rLSE[2][BQ], rDEL[2][BQ], rPRE[2][BQ], rPREL[2][BQ];
     __shared__ float kPHI[BK];
 
-    const int tid = threadIdx.x, w = tid / 64, lane = tid % 64, g = lane / 32, c = lane % 32;
-    const int kt = blockIdx.x;  // heaviest (most query blocks) first
-    const int bh = blockIdx.y, b = bh / p.H, h = bh % p.H;
+    const int tid = threadIdx.x, lane = tid % 64, g = lane / 32, c = lane % 32;
+    const int w = __builtin_amdgcn_readfirstlane(tid / 64);  // wave index, uniform across the wave
+    int rank, bh;
+    xcd_work_item(rank, bh, p.BH);
+    const int kt = rank;  // heaviest (most query blocks) first
+    const int b = bh / p.H, h = bh % p.H;
     const int k0 = kt * BK, kw0 = k0 + 32 * w, s = kw0 + c;
     const int jb = kw0 / G, sb = jb * G;
     const bool wave_active = kw0 < p.T;
@@ -151,6 +154,8 @@ fpa_bwd_kv_kernel(BwdParams p) {
                 rs = fmaxf(Cs, cmid);
                 sv = (rs > ninf()) ? fexp2(sufl - rs) + fexp2(midl - rs) : 0.f;
             }
+            const float Ap = fminf(sufpsi, mid - psi_s);  // min(SUF_s, MID) - psi_s
+            const bool full = (ib + 1) * BQ <= p.T;
             const T *Qt = Qs + buf * TS;
             const T *Dt = dOs + buf * TS;
             const bool diag = (ib == jb);
@@ -163,47 +168,59 @@ fpa_bwd_kv_kernel(BwdParams p) {
                 S[0] = mma_p1_lds_reg<T, D>(zero16(), Qt + (32 * mt + c) * PQ, g, kreg);   // [t][s]
                 dP[0] = mma_p1_lds_reg<T, D>(zero16(), Dt + (32 * mt + c) * PQ, g, vreg);
                 float X[16];
-                if (diag) {
-                    // X_ts = min phi(s, t] inside the block: ascending scan from s + 1.
+                if (diag) diag_x_queries(X, r, phiblk, mt, sr, g);  // X_ts = min phi(s, t] in the block
+                if (!diag) {
+                    // Off the diagonal block every key is valid and every query is later than
+                    // every key; only the rows of a ragged last block are past T.
 #pragma unroll
-                    for (int j = 0; j < 16; ++j) X[j] = pinf();
+                    for (int jq = 0; jq < 4; ++jq) {
+                        const int t4 = 32 * mt + 8 * jq + 4 * g;
+                        const f32x4 lse4 = *reinterpret_cast<const f32x4 *>(&rLSE[buf][t4]);
+                        const f32x4 del4 = *reinterpret_cast<const f32x4 *>(&rDEL[buf][t4]);
+                        const f32x4 pre4 = *reinterpret_cast<const f32x4 *>(&rPRE[buf][t4]);
+                        const f32x4 prl4 = *reinterpret_cast<const f32x4 *>(&rPREL[buf][t4]);
 #pragma unroll
-                    for (int uu = 0; uu < 32; ++uu) {
-                        const int u = 32 * mt + uu;
-                        r = (u > sr) ? fminf(r, phiblk[u]) : r;
-                        const int gg = (uu >> 2) & 1, j = (uu >> 3) * 4 + (uu & 3);
-                        if (gg == g) X[j] = r;
+                        for (int e = 0; e < 4; ++e) {
+                            const int j = 4 * jq + e;
+                            const float x = fminf(Ap, pre4[e] - psi_s);   // min(SUF_s, MID, PRE_t) - psi_s
+                            const float xm = fminf(x, 0.f);
+                            float P = fexp2(fmaf(S[0][j], p.sc2, fmaf(betal, xm, -lse4[e])));
+                            if (!full) P = (ib * BQ + t4 + e < p.T) ? P : 0.f;
+                            const float dS = P * (dP[0][j] - del4[e]);
+                            const float gg = (x <= 0.f) ? dS : 0.f;
+                            gsum += gg;
+                            dbacc = fmaf(gg, x, dbacc);
+                            wblk = fmaf(gg, frcp(sv + fexp2(prl4[e] - rs)), wblk);
+                            S[0][j] = P;
+                            dP[0][j] = dS;
+                        }
                     }
-                }
+                } else {
 #pragma unroll
-                for (int jq = 0; jq < 4; ++jq) {
-                    const int t4 = 32 * mt + 8 * jq + 4 * g;
-                    const f32x4 lse4 = *reinterpret_cast<const f32x4 *>(&rLSE[buf][t4]);
-                    const f32x4 del4 = *reinterpret_cast<const f32x4 *>(&rDEL[buf][t4]);
-                    const f32x4 pre4 = *reinterpret_cast<const f32x4 *>(&rPRE[buf][t4]);
-                    const f32x4 prl4 = *reinterpret_cast<const f32x4 *>(&rPREL[buf][t4]);
-                    f32x4 g4;
+                    for (int jq = 0; jq < 4; ++jq) {
+                        const int t4 = 32 * mt + 8 * jq + 4 * g;
+                        const f32x4 lse4 = *reinterpret_cast<const f32x4 *>(&rLSE[buf][t4]);
+                        const f32x4 del4 = *reinterpret_cast<const f32x4 *>(&rDEL[buf][t4]);
+                        f32x4 g4;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int j = 4 * jq + e;
-                        const int t = ib * BQ + t4 + e;
-                        const bool valid = (t < p.T) && (t >= s) && s_valid;
-                        const bool strict = valid && (t > s);
-                        const float x = diag ? X[j] - psi_s : fminf(sufpsi, fminf(pre4[e], mid) - psi_s);
-                        const float xm = strict ? fminf(x, 0.f) : 0.f;
-                        const float z = fmaf(S[0][j], p.sc2, fmaf(betal, xm, -lse4[e]));
-                        const float P = valid ? fexp2(z) : 0.f;
-                        const float dS = P * (dP[0][j] - del4[e]);
-                        const float gg = (strict && x <= 0.f) ? dS : 0.f;
-                        gsum += gg;
-                        dbacc = fmaf(dS, xm, dbacc);
-                        if (!diag && rs > ninf()) wblk = fmaf(gg, frcp(sv + fexp2(prl4[e] - rs)), wblk);
-                        g4[e] = gg;
-                        S[0][j] = P;
-                        dP[0][j] = dS;
+                        for (int e = 0; e < 4; ++e) {
+                            const int j = 4 * jq + e;
+                            const int t = ib * BQ + t4 + e;
+                            const bool valid = (t < p.T) && (t >= s) && s_valid;
+                            const bool strict = valid && (t > s);
+                            const float x = X[j] - psi_s;
+                            const float xm = strict ? fminf(x, 0.f) : 0.f;
+                            const float P = valid ? fexp2(fmaf(S[0][j], p.sc2, fmaf(betal, xm, -lse4[e]))) : 0.f;
+                            const float dS = P * (dP[0][j] - del4[e]);
+                            const float gg = (strict && x <= 0.f) ? dS : 0.f;
+                            gsum += gg;
+                            dbacc = fmaf(dS, xm, dbacc);  // x is +inf where the range is empty
+                            g4[e] = gg;
+                            S[0][j] = P;
+                            dP[0][j] = dS;
+                        }
+                        if (s_valid) *reinterpret_cast<f32x4 *>(p.gd + ((brow + jb) * G + sr) * G + t4) = g4;
                     }
-                    if (diag && s_valid)
-                        *reinterpret_cast<f32x4 *>(p.gd + ((brow + jb) * G + sr) * G + t4) = g4;
                 }
                 // dV^T[d][s] += dO^T[d][t] P[t][s];  dK^T[d][s] += Q^T[d][t] dS[t][s]
 #pragma unroll

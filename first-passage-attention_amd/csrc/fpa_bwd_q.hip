@@ -26,9 +26,12 @@ fpa_bwd_q_kernel(BwdParams p) {
     __shared__ __attribute__((aligned(16))) T Vs[2 * TS];
     __shared__ __attribute__((aligned(16))) float kSP[2][BK], kPSI[2][BK], kSUFL[2][BK], kPHI[2][BK];
 
-    const int tid = threadIdx.x, w = tid / 64, lane = tid % 64, g = lane / 32, c = lane % 32;
-    const int qt = gridDim.x - 1 - blockIdx.x;  // longest rows first
-    const int bh = blockIdx.y, b = bh / p.H, h = bh % p.H;
+    const int tid = threadIdx.x, lane = tid % 64, g = lane / 32, c = lane % 32;
+    const int w = __builtin_amdgcn_readfirstlane(tid / 64);  // wave index, uniform across the wave
+    int rank, bh;
+    xcd_work_item(rank, bh, p.BH);
+    const int qt = gridDim.x - 1 - rank;  // longest rows first
+    const int b = bh / p.H, h = bh % p.H;
     const int q0 = qt * BM, qw0 = q0 + 32 * w, tq = qw0 + c;
     const int ib = qw0 / G;
     const bool wave_active = qw0 < p.T;
@@ -107,6 +110,7 @@ fpa_bwd_q_kernel(BwdParams p) {
             const float mterm = fexp2(midl - ct) + prel_ct;
             const float Y = fminf(pre, mid);
             const bool diag = (jb == ib);
+            const bool full = qw0 + 32 <= p.T;
             const int tr = tq - s0;
             const T *Kt = Ks + buf * TS;
             const T *Vt = Vs + buf * TS;
@@ -117,40 +121,44 @@ fpa_bwd_q_kernel(BwdParams p) {
                 S[0] = mma_p1_lds_reg<T, D>(zero16(), Kt + (32 * mt + c) * PK, g, qreg);   // [s][t]
                 dP[0] = mma_p1_lds_reg<T, D>(zero16(), Vt + (32 * mt + c) * PK, g, doreg);
                 float X[16];
-                if (diag) {
-                    // X_ts = min phi(s, t] inside the block: descending scan down to s + 1.
+                if (diag) diag_x_keys(X, r, kPHI[buf], mt, tr, g);  // X_ts = min phi(s, t] in the block
+                if (!diag) {
+                    // Off the diagonal block every key is valid and earlier than every query;
+                    // only query rows past T (ragged last block) are masked.
 #pragma unroll
-                    for (int j = 0; j < 16; ++j) X[j] = pinf();
+                    for (int jq = 0; jq < 4; ++jq) {
+                        const int s4 = 32 * mt + 8 * jq + 4 * g;
+                        const f32x4 sp4 = *reinterpret_cast<const f32x4 *>(&kSP[buf][s4]);
+                        const f32x4 psi4 = *reinterpret_cast<const f32x4 *>(&kPSI[buf][s4]);
+                        const f32x4 sfl4 = *reinterpret_cast<const f32x4 *>(&kSUFL[buf][s4]);
 #pragma unroll
-                    for (int uu = 32; uu >= 1; --uu) {
-                        const int u = 32 * mt + uu;  // key u - 1 gets min phi[u .. t]
-                        if (u < G) r = (u <= tr) ? fminf(r, kPHI[buf][u]) : r;
-                        const int sr = uu - 1, gg = (sr >> 2) & 1, j = (sr >> 3) * 4 + (sr & 3);
-                        if (gg == g) X[j] = r;
-                    }
-                }
-#pragma unroll
-                for (int jq = 0; jq < 4; ++jq) {
-                    const int s4 = 32 * mt + 8 * jq + 4 * g;
-                    const f32x4 sp4 = *reinterpret_cast<const f32x4 *>(&kSP[buf][s4]);
-                    const f32x4 psi4 = *reinterpret_cast<const f32x4 *>(&kPSI[buf][s4]);
-                    const f32x4 sfl4 = *reinterpret_cast<const f32x4 *>(&kSUFL[buf][s4]);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int j = 4 * jq + e;
-                        const int s = s0 + s4 + e;
-                        const bool valid = t_valid && (s <= tq);
-                        const bool strict = valid && (s < tq);
-                        const float x = diag ? X[j] - psi4[e] : fminf(sp4[e], Y - psi4[e]);
-                        const float xm = strict ? fminf(x, 0.f) : 0.f;
-                        const float z = fmaf(S[0][j], p.sc2, fmaf(betal, xm, -lse));
-                        const float P = valid ? fexp2(z) : 0.f;
-                        const float dS = P * (dP[0][j] - del);
-                        if (!diag) {
-                            const float gg = (strict && x <= 0.f) ? dS : 0.f;
+                        for (int e = 0; e < 4; ++e) {
+                            const int j = 4 * jq + e;
+                            const float x = fminf(sp4[e], Y - psi4[e]);   // min(SUF_s, MID, PRE_t) - psi_s
+                            const float xm = fminf(x, 0.f);
+                            float P = fexp2(fmaf(S[0][j], p.sc2, fmaf(betal, xm, -lse)));
+                            if (!full) P = t_valid ? P : 0.f;
+                            const float dS = P * (dP[0][j] - del);
+                            const float gg = (x <= 0.f) ? dS : 0.f;
                             racc = fmaf(gg, frcp(fexp2(sfl4[e] - ct) + mterm), racc);
+                            S[0][j] = dS;
                         }
-                        S[0][j] = dS;
+                    }
+                } else {
+#pragma unroll
+                    for (int jq = 0; jq < 4; ++jq) {
+                        const int s4 = 32 * mt + 8 * jq + 4 * g;
+                        const f32x4 psi4 = *reinterpret_cast<const f32x4 *>(&kPSI[buf][s4]);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int j = 4 * jq + e;
+                            const int s = s0 + s4 + e;
+                            const bool valid = t_valid && (s <= tq);
+                            const bool strict = valid && (s < tq);
+                            const float xm = strict ? fminf(X[j] - psi4[e], 0.f) : 0.f;
+                            const float P = valid ? fexp2(fmaf(S[0][j], p.sc2, fmaf(betal, xm, -lse))) : 0.f;
+                            S[0][j] = P * (dP[0][j] - del);
+                        }
                     }
                 }
                 // dQ^T[d][t] += K^T[d][s] dS^T[s][t]   (K read transposed from its natural layout)
@@ -190,7 +198,7 @@ fpa_bwd_q_kernel(BwdParams p) {
 template <typename T, int D>
 static hipError_t launch_q_t(const BwdParams &p, hipStream_t s) {
     const int nqt = (p.T + 127) / 128;
-    constexpr int WPE = (D >= 128 && sizeof(T) == 4) ? 1 : 2;
+    constexpr int WPE = (D >= 128) ? 1 : 2;
     hipLaunchKernelGGL((fpa_bwd_q_kernel<T, D, WPE>), dim3(nqt, p.BH), dim3(NTHREADS), 0, s, p);
     return hipGetLastError();
 }

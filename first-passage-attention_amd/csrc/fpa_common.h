@@ -209,6 +209,47 @@ __device__ __forceinline__ f32x16 mma_p2_p3(f32x16 acc, const f32x16 (&c)[NT], c
 }
 
 // ---------------------------------------------------------------------------
+// In-block range minimum X = min phi(s, t] for the accumulator registers of one 32-row
+// tile of a diagonal 64-block (phi = the block's 64 values, +inf past T).  Branch-free:
+// the running minimum is kept for every step and each register selects its step by
+// lane group.  Entries whose range is empty hold garbage and must be masked by the caller.
+// ---------------------------------------------------------------------------
+
+// Lane = query tr (0..63 in the block); registers = keys 32*mt + acc_row(j, g).  Descending
+// scan; `r` carries min phi[32*mt + 33 .. tr] in and min phi[32*mt + 1 .. tr] out.
+__device__ __forceinline__ void diag_x_keys(float (&X)[16], float &r, const float *phi, int mt, int tr, int g) {
+    float rr[33];
+#pragma unroll
+    for (int k = 32; k >= 1; --k) {
+        const int u = 32 * mt + k;
+        if (u < G) r = fminf(r, (u <= tr) ? phi[u] : pinf());
+        rr[k] = r;  // min phi[u .. tr]: the value for key u - 1
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int k0 = 8 * (j / 4) + (j % 4);
+        X[j] = g ? rr[k0 + 5] : rr[k0 + 1];
+    }
+}
+
+// Lane = key sr (0..63 in the block); registers = queries 32*mt + acc_row(j, g).  Ascending
+// scan; `r` carries min phi[sr+1 .. 32*mt - 1] in and min phi[sr+1 .. 32*mt + 31] out.
+__device__ __forceinline__ void diag_x_queries(float (&X)[16], float &r, const float *phi, int mt, int sr, int g) {
+    float rr[32];
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+        const int u = 32 * mt + k;
+        r = fminf(r, (u > sr) ? phi[u] : pinf());
+        rr[k] = r;  // min phi[sr+1 .. u]: the value for query u
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int k0 = 8 * (j / 4) + (j % 4);
+        X[j] = g ? rr[k0 + 4] : rr[k0];
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Register prefetch of an NR x D tile of a (B, H, T, D)-strided tensor (rows row0 + r,
 // zero past T), stored afterwards into a natural-layout LDS tile of the given pitch.
 // ---------------------------------------------------------------------------
@@ -219,6 +260,15 @@ template <typename T, int D, int NR> struct TileRegs {
     static constexpr int PER = (NCH + NTHREADS - 1) / NTHREADS;
     f32x4 r[PER];
     __device__ __forceinline__ void load(const T *base, int64_t st, int row0, int T_) {
+        if (row0 + NR <= T_ && NCH % NTHREADS == 0) {  // full tile: no per-row guard
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int idx = threadIdx.x + i * NTHREADS;
+                const int row = idx / CPR, cc = idx % CPR;
+                r[i] = *reinterpret_cast<const f32x4 *>(base + (int64_t)(row0 + row) * st + cc * CE);
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int idx = threadIdx.x + i * NTHREADS;
@@ -246,6 +296,22 @@ __device__ __forceinline__ void load_row_p1(OpRow<T, D> &dst, const T *rowp, boo
         p1_load_row<T, D>(dst, rowp, g);
     else
         p1_zero<T, D>(dst);
+}
+
+// Work item of this workgroup in a grid of (ntiles, BH): rank 0 is the heaviest tile.
+// Workgroups are dispatched in linear order, round-robin over the 8 XCDs of the chip; when
+// BH is a multiple of 8 every head is pinned to one XCD (its K/V stay in that XCD's L2)
+// and each XCD takes its heads' tiles heaviest first.
+__device__ __forceinline__ void xcd_work_item(int &rank, int &bh, int BH) {
+    const int L = blockIdx.x + gridDim.x * blockIdx.y;
+    if ((BH & 7) == 0) {
+        const int xcd = L & 7, k = L >> 3, hpx = BH >> 3;
+        rank = k / hpx;
+        bh = (k % hpx) * 8 + xcd;
+    } else {
+        rank = blockIdx.x;
+        bh = blockIdx.y;
+    }
 }
 
 // Sum over the 64 lanes of a wave, fixed order (butterfly).

@@ -105,9 +105,12 @@ fpa_fwd_kernel(FwdParams p) {
     __shared__ __attribute__((aligned(16))) T Vs[2 * TS + (DT - D)];
     __shared__ __attribute__((aligned(16))) float cA[2][BN], cP[2][BN], cPHI[2][BN];
 
-    const int tid = threadIdx.x, w = tid / 64, lane = tid % 64, g = lane / 32, c = lane % 32;
-    const int qt = gridDim.x - 1 - blockIdx.x;  // longest rows first
-    const int bh = blockIdx.y, b = bh / p.H, h = bh % p.H;
+    const int tid = threadIdx.x, lane = tid % 64, g = lane / 32, c = lane % 32;
+    const int w = __builtin_amdgcn_readfirstlane(tid / 64);  // wave index, uniform across the wave
+    int rank, bh;
+    xcd_work_item(rank, bh, p.BH);
+    const int qt = gridDim.x - 1 - rank;  // longest rows first
+    const int b = bh / p.H, h = bh % p.H;
     const int q0 = qt * BM, qw0 = q0 + 32 * w, tq = qw0 + c;
     const int ib = qw0 / G;
     const bool wave_active = qw0 < p.T;
@@ -190,35 +193,21 @@ fpa_fwd_kernel(FwdParams p) {
                         }
                     }
             } else {
-                // Diagonal block: X_ts = min phi(s, t] inside the block, by a descending scan.
+                // Diagonal block: X_ts = min phi(s, t] inside the block.
                 const int tr = tq - s0;
                 float X[2][16];
-#pragma unroll
-                for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-                    for (int j = 0; j < 16; ++j) X[mt][j] = pinf();
                 float r = pinf();
-#pragma unroll
-                for (int u = BN - 1; u >= 1; --u) {
-                    r = (u <= tr) ? fminf(r, cPHI[buf][u]) : r;
-                    const int sr = u - 1, mt = sr >> 5, jj = sr & 31;
-                    const int gg = (jj >> 2) & 1, j = (jj >> 3) * 4 + (jj & 3);
-                    if (gg == g) X[mt][j] = r;
-                }
+                diag_x_keys(X[1], r, cPHI[buf], 1, tr, g);
+                diag_x_keys(X[0], r, cPHI[buf], 0, tr, g);
 #pragma unroll
                 for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
                     for (int j = 0; j < 16; ++j) {
                         const int sr = 32 * mt + acc_row(j, g);
-                        float z;
-                        if (sr > tr || s0 + sr >= p.T)
-                            z = ninf();
-                        else if (sr == tr)
-                            z = s[mt][j] * p.sc2;
-                        else
-                            z = fmaf(s[mt][j], p.sc2,
-                                     __builtin_amdgcn_fmed3f(0.f, fmaf(betal, X[mt][j], -cP[buf][sr]), E));
-                        s[mt][j] = z;
+                        const float b2 = (sr < tr) ? __builtin_amdgcn_fmed3f(0.f, fmaf(betal, X[mt][j], -cP[buf][sr]), E)
+                                                   : 0.f;  // b_tt = 0
+                        const float z = fmaf(s[mt][j], p.sc2, b2);
+                        s[mt][j] = (sr > tr || s0 + sr >= p.T) ? ninf() : z;
                     }
             }
 
@@ -289,7 +278,7 @@ fpa_fwd_kernel(FwdParams p) {
 template <typename T, int D>
 static hipError_t launch_fwd_t(const FwdParams &p, hipStream_t s) {
     const int nqt = (p.T + 127) / 128;
-    constexpr int WPE = (sizeof(T) == 4 && D >= 128) ? 1 : 2;
+    constexpr int WPE = (D >= 128) ? 1 : 2;
     hipLaunchKernelGGL((fpa_fwd_kernel<T, D, WPE>), dim3(nqt, p.BH), dim3(NTHREADS), 0, s, p);
     return hipGetLastError();
 }
