@@ -172,8 +172,7 @@ def main():
         "fpa_bwd_prep": (time_call(ba, _hip.run_bwd, _lib.FPA_BWD_DELTA), 0),
         "fpa_bwd_kv_kernel": (time_call(ba, _hip.run_bwd, _lib.FPA_BWD_KEYS), 8 * D * P),
         "fpa_bwd_q_kernel": (time_call(ba, _hip.run_bwd, _lib.FPA_BWD_QUERIES), 2 * D * P),
-        "fpa_bwd_combine": (time_call(ba, _hip.run_bwd, _lib.FPA_BWD_PHI), 0),
-        "fpa_bwd_dbeta": (time_call(ba, _hip.run_bwd, _lib.FPA_BWD_BETA), 0),
+        "fpa_bwd_combine_kernel": (time_call(ba, _hip.run_bwd, _lib.FPA_BWD_PHI), 0),
     }
     dom = max(kernels, key=lambda n: kernels[n][0])
     dom_ms, dom_flops = kernels[dom]

@@ -111,6 +111,7 @@ int fpa_fwd(const FpaFwdArgs *a, void *stream) {
     StatsParams sp;
     sp.phi = a->phi; sp.sphi = s3(a->sphi);
     sp.psi = a->psi; sp.spsi = s3(a->spsi);
+    sp.beta = a->beta;
     sp.state = a->state;
     sp.H = (int)a->H; sp.T = (int)a->T; sp.TP = (int)TP; sp.NB = (int)(TP / G); sp.BH = (int)(a->B * a->H);
     sp.il2 = LOG2E / a->tau;
@@ -177,8 +178,8 @@ int fpa_bwd(const FpaBwdArgs *a, void *stream) {
         return hip_fail(e, "fpa_bwd_kv launch");
     if ((ph & FPA_BWD_QUERIES) && (e = launch_bwd_q(p, a->dtype, (int)a->D, s)) != hipSuccess)
         return hip_fail(e, "fpa_bwd_q launch");
-    if ((ph & FPA_BWD_PHI) && (e = launch_bwd_combine(p, s)) != hipSuccess) return hip_fail(e, "fpa_bwd_combine launch");
-    if ((ph & FPA_BWD_BETA) && (e = launch_bwd_dbeta(p, s)) != hipSuccess) return hip_fail(e, "fpa_bwd_dbeta launch");
+    if ((ph & (FPA_BWD_PHI | FPA_BWD_BETA)) && (e = launch_bwd_combine(p, s)) != hipSuccess)
+        return hip_fail(e, "fpa_bwd_combine launch");
     return FPA_OK;
 }
 

@@ -8,10 +8,17 @@
 //                   + sum_{t>=u, t in U} 2^{a_u - c_t} R_t          query-block part
 //                   + 2^{a_u - c_U} sum_{j<U<i} 2^{c_U - cmid(i,j)} TBUF[i][j]   middle blocks
 //                   + sum_{s<u<=t, s,t in U} g_ts 2^{a_u} / Z_ts )  in-block pairs
-// with C_s = max a over (s, end of U), c_t = max a over [start of U, t], c_U = max a
-// over U, cmid(i, j) = max a over blocks j+1..i-1.  The in-block part runs, per
-// column s, the recurrences lz(u) = log2 sum_{s<u'<=u} 2^{a_u'},
-// lam(u) = g_us + 2^{lz(u) - lz(u+1)} lam(u+1), contribution 2^{a_u - lz(u)} lam(u).
+// with C_s = max a over (s, end of U), c_t = max a over [start of U, t], c_U = max a over U,
+// cmid(i, j) = max a over blocks j+1..i-1.
+//
+// In-block pairs, per column s: with m(u) = max a over (s, u] and
+// Z(u) = sum_{s<v<=u} 2^{a_v - m(u)} (>= 1), the forward chain is
+// Z(u) = Z(u-1) 2^{m(u-1) - m(u)} + 2^{a_u - m(u)}, and the reverse chain
+// lam(u) = g_us + rho(u) lam(u+1) with rho(u) = Z(u) 2^{m(u) - m(u+1)} / Z(u+1) gives the
+// contribution 2^{a_u - m(u)} lam(u) / Z(u) to u.  Only FMAs sit on the dependent chains,
+// and the 64 steps are split over the four waves of the workgroup.
+//
+// dbeta[h] is summed (fixed order) by the workgroup of block 0 of batch 0 of head h.
 // All sums run in a fixed order: the result is bit-reproducible.
 #include "fpa_common.h"
 #include "fpa_params.h"
@@ -34,19 +41,33 @@ __device__ __forceinline__ float block_sum_256(float x, float *red) {
 }
 
 __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) {
-    __shared__ float sA[G], sC[G], sc[G], sW[G], sR[G], sP[G];
-    __shared__ float lz[G][G + 1];
-    __shared__ float contrib[G][G + 1];
-    __shared__ float Amax[MAXNB], Bmax[MAXNB];
+    __shared__ float sA[G], sC[G], sc[G], sW[G], sR[G];
+    __shared__ float segM[4][G], segZ[4][G], segM2[4][G], segZ2[4][G], segA[4][G], segB[4][G], pp[4][G];
+    __shared__ float sBM[MAXNB];             // max a of every block of the head
+    __shared__ float scanA[MAXNB], scanB[MAXNB];
+    __shared__ float contrib[G][G + 1];      // [u][s]
     __shared__ float red[NTHREADS];
 
-    const int U = blockIdx.x, bh = blockIdx.y, h = bh % p.H;
-    const int tid = threadIdx.x, lane = tid % 64, w = tid / 64;
+    const int U = blockIdx.x, bh = blockIdx.y, b = bh / p.H, h = bh % p.H;
+    const int tid = threadIdx.x, lane = tid % 64;
+    const int w = __builtin_amdgcn_readfirstlane(tid / 64);
     const int sb = U * G, last = min(G - 1, p.T - 1 - sb);
     const StateLayout L{p.BH, p.TP, p.NB};
     const int64_t rowbase = (int64_t)bh * p.TP;
     const int64_t brow = (int64_t)bh * p.NB;
     const float il2 = p.il2;
+    const int NB = p.NB;
+
+    if (U == 0 && b == 0) {  // dbeta[h] = sum over batches and key-side partials
+        const int n = p.NKV * 4;
+        float acc = 0.f;
+        for (int bb = 0; bb < p.B; ++bb) {
+            const float *src = p.dbp + ((int64_t)(bb * p.H + h) * p.NKV) * 4;
+            for (int i = tid; i < n; i += NTHREADS) acc += src[i];
+        }
+        const float tot = block_sum_256(acc, red);
+        if (tid == 0) p.dbeta[h] = tot;
+    }
 
     if (tid < G) {
         const int64_t r = rowbase + sb + tid;
@@ -59,97 +80,154 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
         sW[tid] = p.wsum[r];
         sR[tid] = p.rsum[r];
     }
-    const float cU = -p.state[L.bplane(BP_MIN) + brow + U] * il2;
-    const int nI = p.NB - 1 - U;
-    const int npairs = U * nI;
-    if (npairs > 0) {
-        if (tid == 0) {
-            float run = ninf();
-            for (int jb = U - 1; jb >= 0; --jb) {
-                Amax[jb] = run;
-                run = fmaxf(run, -p.state[L.bplane(BP_MIN) + brow + jb] * il2);
-            }
-        } else if (tid == 64) {
-            float run = ninf();
-            for (int ib = U + 1; ib < p.NB; ++ib) {
-                Bmax[ib] = run;
-                run = fmaxf(run, -p.state[L.bplane(BP_MIN) + brow + ib] * il2);
-            }
-        }
+    for (int i = tid; i < NB; i += NTHREADS) {
+        const float bm = -p.state[L.bplane(BP_MIN) + brow + i] * il2;
+        sBM[i] = bm;
+        scanA[i] = (i < U) ? bm : ninf();  // suffix maxima over [i, U)
+        scanB[i] = (i > U) ? bm : ninf();  // prefix maxima over (U, i]
     }
     __syncthreads();
-    float acc = 0.f;
-    for (int idx = tid; idx < npairs; idx += NTHREADS) {
-        const int jb = idx / nI, ib = U + 1 + idx % nI;
-        const float cm = fmaxf(fmaxf(Amax[jb], cU), Bmax[ib]);
-        const float *tb = p.tbuf + ((brow + ib) * p.NB + jb) * 2;
-        acc += fexp2(cU - cm) * (tb[0] + tb[1]);
-    }
-    const float SU = block_sum_256(acc, red);
-
-    if (w == 0) {
-        // In-block recurrences, one column s per lane.
-        const int s = lane;
-        const float *gcol = p.gd + ((brow + U) * G + s) * G;
-        float run = ninf();
-        for (int u = 0; u < G; ++u) {
-            if (u > s && u <= last) run = lse2_pair(run, sA[u]);
-            lz[s][u] = run;
+    const float cU = sBM[U];
+    const int nI = NB - 1 - U;
+    const int npairs = U * nI;
+    float SU = 0.f;
+    if (npairs > 0) {
+        for (int off = 1; off < NB; off <<= 1) {  // Hillis-Steele scans in place, two phases per step
+            float va[MAXNB / NTHREADS], vb[MAXNB / NTHREADS];
+            int k = 0;
+            for (int i = tid; i < NB; i += NTHREADS, ++k) {
+                va[k] = (i + off < NB) ? fmaxf(scanA[i], scanA[i + off]) : scanA[i];
+                vb[k] = (i >= off) ? fmaxf(scanB[i], scanB[i - off]) : scanB[i];
+            }
+            __syncthreads();
+            k = 0;
+            for (int i = tid; i < NB; i += NTHREADS, ++k) {
+                scanA[i] = va[k];
+                scanB[i] = vb[k];
+            }
+            __syncthreads();
         }
-        float lam = 0.f;
-        for (int u = G - 1; u >= 0; --u) {
+        // cmid(ib, jb) = max(A_jb, c_U, B_ib), A_jb = max over (jb, U) = scanA[jb + 1],
+        // B_ib = max over (U, ib) = scanB[ib - 1].  Consecutive threads read consecutive jb.
+        float acc = 0.f;
+        for (int idx = tid; idx < npairs; idx += NTHREADS) {
+            const int ib = U + 1 + idx / U, jb = idx % U;
+            const float cm = fmaxf(fmaxf(scanA[jb + 1], cU), scanB[ib - 1]);
+            const float *tb = p.tbuf + ((brow + ib) * NB + jb) * 2;
+            acc += fexp2(cU - cm) * (tb[0] + tb[1]);
+        }
+        SU = block_sum_256(acc, red);
+    }
+
+    // In-block pairs.  Lane s owns column s; wave w owns the steps u in [16w, 16w + 16).
+    // Each wave runs its segment of both chains locally, the segments are joined through LDS
+    // (forward states combine associatively, reverse affine maps compose), and each wave then
+    // reruns its segment from the joined state.
+    {
+        const int s = lane, u0 = 16 * w;
+        const float *gcol = p.gd + ((brow + U) * G + s) * G;
+        float m = ninf(), Z = 0.f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int u = u0 + k;
+            if (u > s && u <= last) {
+                const float mn = fmaxf(m, sA[u]);
+                Z = fmaf(Z, fexp2(m - mn), fexp2(sA[u] - mn));
+                m = mn;
+            }
+        }
+        segM[w][s] = m;
+        segZ[w][s] = Z;
+        __syncthreads();
+        m = ninf();
+        Z = 0.f;
+        for (int v = 0; v < w; ++v) {  // state entering this segment
+            const float m2 = segM[v][s], z2 = segZ[v][s];
+            if (m2 > ninf()) {
+                const float mn = fmaxf(m, m2);
+                Z = fmaf(Z, fexp2(m - mn), z2 * fexp2(m2 - mn));
+                m = mn;
+            }
+        }
+        float mv[16], zv[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int u = u0 + k;
+            if (u > s && u <= last) {
+                const float mn = fmaxf(m, sA[u]);
+                Z = fmaf(Z, fexp2(m - mn), fexp2(sA[u] - mn));
+                m = mn;
+            }
+            mv[k] = m;
+            zv[k] = Z;
+        }
+        segM2[w][s] = mv[0];
+        segZ2[w][s] = zv[0];
+        __syncthreads();
+        const float mnext = (w < 3) ? segM2[w + 1][s] : 0.f;
+        const float znext = (w < 3) ? segZ2[w + 1][s] : 1.f;
+        float rho[16], gv[16];
+        float lam = 0.f, Bc = 1.f;
+#pragma unroll
+        for (int k = 15; k >= 0; --k) {
+            const int u = u0 + k;
+            rho[k] = 0.f;
+            gv[k] = 0.f;
+            if (u > s && u <= last) {
+                const float m1 = (k < 15) ? mv[k + 1] : mnext;
+                const float z1 = (k < 15) ? zv[k + 1] : znext;
+                rho[k] = (u < last) ? zv[k] * fexp2(mv[k] - m1) * frcp(z1) : 0.f;
+                gv[k] = gcol[u];
+                lam = fmaf(rho[k], lam, gv[k]);
+                Bc *= rho[k];
+            }
+        }
+        segA[w][s] = lam;
+        segB[w][s] = Bc;
+        __syncthreads();
+        lam = 0.f;
+        for (int v = 3; v > w; --v) lam = fmaf(segB[v][s], lam, segA[v][s]);  // lambda entering from above
+#pragma unroll
+        for (int k = 15; k >= 0; --k) {
+            const int u = u0 + k;
             float cval = 0.f;
             if (u > s && u <= last) {
-                const float rho = (u + 1 <= last) ? fexp2(lz[s][u] - lz[s][u + 1]) : 0.f;
-                lam = gcol[u] + rho * lam;
-                cval = fexp2(sA[u] - lz[s][u]) * lam;
+                lam = fmaf(rho[k], lam, gv[k]);
+                cval = fexp2(sA[u] - mv[k]) * frcp(zv[k]) * lam;
             }
             contrib[u][s] = cval;
         }
-    } else if (w == 1) {
-        const int u = lane;
-        float v = 0.f;
+    }
+    {
+        // Key-block and query-block parts: lane u, wave w sums its 16 of the 64 terms.
+        const int u = lane, v0 = 16 * w;
+        float part = 0.f;
         if (u <= last) {
             const float au = sA[u];
-            float p1 = 0.f, p2 = 0.f;
-            for (int s = 0; s < u; ++s) p1 += fexp2(au - sC[s]) * sW[s];
-            for (int t = u; t <= last; ++t) p2 += fexp2(au - sc[t]) * sR[t];
-            v = p1 + p2 + ((npairs > 0) ? fexp2(au - cU) * SU : 0.f);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                const int v = v0 + k;
+                if (v < u) part = fmaf(fexp2(au - sC[v]), sW[v], part);
+                if (v >= u && v <= last) part = fmaf(fexp2(au - sc[v]), sR[v], part);
+            }
         }
-        sP[u] = v;
+        pp[w][u] = part;
     }
     __syncthreads();
     if (w == 0) {
         const int u = lane;
         if (u <= last) {
+            float tot = ((pp[0][u] + pp[1][u]) + (pp[2][u] + pp[3][u]));
+            if (npairs > 0) tot += fexp2(sA[u] - cU) * SU;
             float p4 = 0.f;
             for (int s = 0; s < u; ++s) p4 += contrib[u][s];
-            p.dphi[(int64_t)bh * p.T + sb + u] = p.beta[h] * (sP[u] + p4);
+            p.dphi[(int64_t)bh * p.T + sb + u] = p.beta[h] * (tot + p4);
         }
     }
-}
-
-// dbeta[h] = sum over batches and key-side partials, fixed order.
-__global__ void __launch_bounds__(NTHREADS) fpa_bwd_dbeta_kernel(BwdParams p) {
-    __shared__ float red[NTHREADS];
-    const int h = blockIdx.x;
-    const int n = p.NKV * 4;
-    float acc = 0.f;
-    for (int b = 0; b < p.B; ++b) {
-        const float *src = p.dbp + ((int64_t)(b * p.H + h) * p.NKV) * 4;
-        for (int i = threadIdx.x; i < n; i += NTHREADS) acc += src[i];
-    }
-    const float tot = block_sum_256(acc, red);
-    if (threadIdx.x == 0) p.dbeta[h] = tot;
 }
 
 hipError_t launch_bwd_combine(const BwdParams &p, hipStream_t s) {
     hipLaunchKernelGGL(fpa_bwd_combine_kernel, dim3(p.NB, p.BH), dim3(NTHREADS), 0, s, p);
-    return hipGetLastError();
-}
-
-hipError_t launch_bwd_dbeta(const BwdParams &p, hipStream_t s) {
-    hipLaunchKernelGGL(fpa_bwd_dbeta_kernel, dim3(p.H), dim3(NTHREADS), 0, s, p);
     return hipGetLastError();
 }
 

@@ -12,8 +12,19 @@
 //   W_s     = sum_{t outside blk(s)} g_ts 2^{C_s} / Z_ts   (key-block soft-min sums)
 //   TBUF    = middle-block soft-min sums per (query block, key block, key half)
 // and writes the in-block gated dS to GD for the in-block soft-min recurrence.
+#include <type_traits>
+
 #include "fpa_common.h"
 #include "fpa_params.h"
+
+// Tuning knobs (build-time): waves per SIMD of the fp16 D <= 64 key-side kernel, and whether
+// well-conditioned tiles use the shared-reference soft-min path.
+#ifndef FPA_KV_WPE
+#define FPA_KV_WPE 2
+#endif
+#ifndef FPA_KV_FAST
+#define FPA_KV_FAST 0
+#endif
 
 namespace fpa {
 
@@ -59,6 +70,7 @@ fpa_bwd_kv_kernel(BwdParams p) {
     __shared__ __attribute__((aligned(16))) T dOs[2 * TS + (DT - D)];
     __shared__ __attribute__((aligned(16))) float rLSE[2][BQ], rDEL[2][BQ], rPRE[2][BQ], rPREL[2][BQ];
     __shared__ float kPHI[BK];
+    __shared__ __attribute__((aligned(16))) float Bw[4][BQ];  // per-wave query factors of the shared-reference path
 
     const int tid = threadIdx.x, lane = tid % 64, g = lane / 32, c = lane % 32;
     const int w = __builtin_amdgcn_readfirstlane(tid / 64);  // wave index, uniform across the wave
@@ -144,6 +156,7 @@ fpa_bwd_kv_kernel(BwdParams p) {
         if (ib + 1 < p.NB) gload(ib + 1);
         if (wave_active && ib >= jb) {
             float rs = ninf(), sv = 0.f;
+            bool fast = false;
             if (ib > jb) {
                 if (ib - 1 > jb) {  // block ib - 1 joins the middle
                     const float bm = p.state[L.bplane(BP_MIN) + brow + ib - 1];
@@ -151,8 +164,20 @@ fpa_bwd_kv_kernel(BwdParams p) {
                     midl = lse2_pair(midl, p.state[L.bplane(BP_LSE) + brow + ib - 1]);
                     cmid = fmaxf(cmid, -bm * p.il2);
                 }
-                rs = fmaxf(Cs, cmid);
-                sv = (rs > ninf()) ? fexp2(sufl - rs) + fexp2(midl - rs) : 0.f;
+                // Shared reference R >= every exponent of the tile; the smallest pair maximum is
+                // at least max(cmid, a of the block's first query).
+                const float cfirst = uniform_f(Cs);  // lane 0 holds the wave's first key: largest C_s
+                const float R = fmaxf(fmaxf(cfirst, cmid), -p.state[L.bplane(BP_MIN) + brow + ib] * p.il2);
+                const float lo = fmaxf(cmid, -p.state[L.plane(PL_PHI) + rowbase + ib * BQ] * p.il2);
+                fast = FPA_KV_FAST && (R - lo) < FAST_SPREAD;
+                if (fast) {
+                    rs = R;  // W_s and TBUF are scaled by 2^{. - R} at the end of the block
+                    sv = fexp2(sufl - R) + fexp2(midl - R);
+                    Bw[w][lane] = fexp2(rPREL[buf][lane] - R);
+                } else {
+                    rs = fmaxf(Cs, cmid);
+                    sv = (rs > ninf()) ? fexp2(sufl - rs) + fexp2(midl - rs) : 0.f;
+                }
             }
             const float Ap = fminf(sufpsi, mid - psi_s);  // min(SUF_s, MID) - psi_s
             const bool full = (ib + 1) * BQ <= p.T;
@@ -172,29 +197,41 @@ fpa_bwd_kv_kernel(BwdParams p) {
                 if (!diag) {
                     // Off the diagonal block every key is valid and every query is later than
                     // every key; only the rows of a ragged last block are past T.
+                    auto offdiag = [&](auto fast_c) {
+                        constexpr bool FAST = decltype(fast_c)::value;
 #pragma unroll
-                    for (int jq = 0; jq < 4; ++jq) {
-                        const int t4 = 32 * mt + 8 * jq + 4 * g;
-                        const f32x4 lse4 = *reinterpret_cast<const f32x4 *>(&rLSE[buf][t4]);
-                        const f32x4 del4 = *reinterpret_cast<const f32x4 *>(&rDEL[buf][t4]);
-                        const f32x4 pre4 = *reinterpret_cast<const f32x4 *>(&rPRE[buf][t4]);
-                        const f32x4 prl4 = *reinterpret_cast<const f32x4 *>(&rPREL[buf][t4]);
+                        for (int jq = 0; jq < 4; ++jq) {
+                            const int t4 = 32 * mt + 8 * jq + 4 * g;
+                            const f32x4 lse4 = *reinterpret_cast<const f32x4 *>(&rLSE[buf][t4]);
+                            const f32x4 del4 = *reinterpret_cast<const f32x4 *>(&rDEL[buf][t4]);
+                            const f32x4 pre4 = *reinterpret_cast<const f32x4 *>(&rPRE[buf][t4]);
+                            const f32x4 zq4 = FAST ? *reinterpret_cast<const f32x4 *>(&Bw[w][t4])
+                                                   : *reinterpret_cast<const f32x4 *>(&rPREL[buf][t4]);
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const int j = 4 * jq + e;
-                            const float x = fminf(Ap, pre4[e] - psi_s);   // min(SUF_s, MID, PRE_t) - psi_s
-                            const float xm = fminf(x, 0.f);
-                            float P = fexp2(fmaf(S[0][j], p.sc2, fmaf(betal, xm, -lse4[e])));
-                            if (!full) P = (ib * BQ + t4 + e < p.T) ? P : 0.f;
-                            const float dS = P * (dP[0][j] - del4[e]);
-                            const float gg = (x <= 0.f) ? dS : 0.f;
-                            gsum += gg;
-                            dbacc = fmaf(gg, x, dbacc);
-                            wblk = fmaf(gg, frcp(sv + fexp2(prl4[e] - rs)), wblk);
-                            S[0][j] = P;
-                            dP[0][j] = dS;
+                            for (int e = 0; e < 4; ++e) {
+                                const int j = 4 * jq + e;
+                                const float x = fminf(Ap, pre4[e] - psi_s);  // min(SUF_s, MID, PRE_t) - psi_s
+                                const float xm = fminf(x, 0.f);
+                                float P = fexp2(fmaf(S[0][j], p.sc2, fmaf(betal, xm, -lse4[e])));
+                                if (!full) P = (ib * BQ + t4 + e < p.T) ? P : 0.f;
+                                const float dS = P * (dP[0][j] - del4[e]);
+                                const float gg = (x <= 0.f) ? dS : 0.f;
+                                gsum += gg;
+                                dbacc = fmaf(gg, x, dbacc);
+                                // Z_ts 2^{-r} = sv + 2^{PREL_t - r}, r shared (FAST) or per key
+                                const float zq = FAST ? zq4[e] : fexp2(zq4[e] - rs);
+                                wblk = fmaf(gg, frcp(sv + zq), wblk);
+                                S[0][j] = P;
+                                dP[0][j] = dS;
+                            }
                         }
-                    }
+                    };
+#if FPA_KV_FAST
+                    if (fast)
+                        offdiag(std::true_type{});
+                    else
+#endif
+                        offdiag(std::false_type{});
                 } else {
 #pragma unroll
                     for (int jq = 0; jq < 4; ++jq) {
@@ -285,7 +322,7 @@ static hipError_t launch_prep_t(const BwdParams &p, hipStream_t s) {
 
 template <typename T, int D>
 static hipError_t launch_kv_t(const BwdParams &p, hipStream_t s) {
-    constexpr int WPE = (D >= 128 || (sizeof(T) == 4 && D >= 64)) ? 1 : 2;
+    constexpr int WPE = (D >= 128 || (sizeof(T) == 4 && D >= 64)) ? 1 : FPA_KV_WPE;
     hipLaunchKernelGGL((fpa_bwd_kv_kernel<T, D, WPE>), dim3(p.NKV, p.BH), dim3(NTHREADS), 0, s, p);
     return hipGetLastError();
 }

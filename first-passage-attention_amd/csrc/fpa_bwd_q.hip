@@ -9,8 +9,19 @@
 // transpose reads), and reduces per query the query-block soft-min sum
 //   R_t = sum_{s outside blk(t)} g_ts 2^{c_t} / Z_ts,   c_t = max a over [start of blk(t), t].
 // The diagonal block (keys and query in one 64-block) uses the in-block range minimum.
+#include <type_traits>
+
 #include "fpa_common.h"
 #include "fpa_params.h"
+
+// Tuning knobs (build-time): waves per SIMD of the D <= 64 query-side kernel, and whether
+// well-conditioned tiles use the shared-reference soft-min path.
+#ifndef FPA_Q_WPE
+#define FPA_Q_WPE 2
+#endif
+#ifndef FPA_Q_FAST
+#define FPA_Q_FAST 1
+#endif
 
 namespace fpa {
 
@@ -25,6 +36,7 @@ fpa_bwd_q_kernel(BwdParams p) {
     __shared__ __attribute__((aligned(16))) T Ks[2 * TS + (DT - D)];
     __shared__ __attribute__((aligned(16))) T Vs[2 * TS];
     __shared__ __attribute__((aligned(16))) float kSP[2][BK], kPSI[2][BK], kSUFL[2][BK], kPHI[2][BK];
+    __shared__ __attribute__((aligned(16))) float Aw[4][BK];  // per-wave key factors of the shared-reference path
 
     const int tid = threadIdx.x, lane = tid % 64, g = lane / 32, c = lane % 32;
     const int w = __builtin_amdgcn_readfirstlane(tid / 64);  // wave index, uniform across the wave
@@ -68,7 +80,10 @@ fpa_bwd_q_kernel(BwdParams p) {
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) dqacc[dt] = zero16();
     float racc = 0.f;
-    float mid = pinf(), midl = ninf();  // over blocks strictly between jb and ib
+    float mid = pinf(), midl = ninf(), cmid = ninf();  // over blocks strictly between jb and ib
+    const int ibc = min(ib, p.NB - 1);  // waves past T keep ib in range for these reads
+    const float a_first = -p.state[L.plane(PL_PHI) + rowbase + ibc * G] * p.il2;  // a of the block's first query
+    const float c_blk = -p.state[L.bplane(BP_MIN) + brow + ibc] * p.il2;          // max a over block ib
 
     TileRegs<T, D, BK> kr, vr;
     float pf_suf = 0.f, pf_psi = 0.f, pf_sufl = 0.f, pf_phi = 0.f;
@@ -104,10 +119,25 @@ fpa_bwd_q_kernel(BwdParams p) {
         if (jb > 0) gload(jb - 1);
         if (wave_active && jb <= ib) {
             if (jb + 1 < ib) {  // block jb + 1 joins the middle
-                mid = fminf(mid, p.state[L.bplane(BP_MIN) + brow + jb + 1]);
+                const float bm = p.state[L.bplane(BP_MIN) + brow + jb + 1];
+                mid = fminf(mid, bm);
                 midl = lse2_pair(midl, p.state[L.bplane(BP_LSE) + brow + jb + 1]);
+                cmid = fmaxf(cmid, -bm * p.il2);
             }
             const float mterm = fexp2(midl - ct) + prel_ct;
+            // Shared reference R >= every exponent of the tile (largest C_s is at the block's first key).
+            bool fast = false;
+            float R = 0.f, bq = 0.f;
+            if (jb < ib) {
+                const float cfirst = -p.state[L.plane(PL_SUF) + rowbase + s0] * p.il2;
+                R = fmaxf(fmaxf(cfirst, cmid), c_blk);
+                fast = FPA_Q_FAST && (R - fmaxf(cmid, a_first)) < FAST_SPREAD;
+                if (fast) {
+                    Aw[w][lane] = fexp2(kSUFL[buf][lane] - R) + fexp2(midl - R);
+                    bq = t_valid ? fexp2(prel - R) : 1.f;  // rows past T: any positive factor (g = 0)
+                }
+            }
+            float rblk = 0.f;  // sum of g / (Z 2^{-R}) over this key block (shared-reference path)
             const float Y = fminf(pre, mid);
             const bool diag = (jb == ib);
             const bool full = qw0 + 32 <= p.T;
@@ -125,25 +155,38 @@ fpa_bwd_q_kernel(BwdParams p) {
                 if (!diag) {
                     // Off the diagonal block every key is valid and earlier than every query;
                     // only query rows past T (ragged last block) are masked.
+                    auto offdiag = [&](auto fast_c) {
+                        constexpr bool FAST = decltype(fast_c)::value;
 #pragma unroll
-                    for (int jq = 0; jq < 4; ++jq) {
-                        const int s4 = 32 * mt + 8 * jq + 4 * g;
-                        const f32x4 sp4 = *reinterpret_cast<const f32x4 *>(&kSP[buf][s4]);
-                        const f32x4 psi4 = *reinterpret_cast<const f32x4 *>(&kPSI[buf][s4]);
-                        const f32x4 sfl4 = *reinterpret_cast<const f32x4 *>(&kSUFL[buf][s4]);
+                        for (int jq = 0; jq < 4; ++jq) {
+                            const int s4 = 32 * mt + 8 * jq + 4 * g;
+                            const f32x4 sp4 = *reinterpret_cast<const f32x4 *>(&kSP[buf][s4]);
+                            const f32x4 psi4 = *reinterpret_cast<const f32x4 *>(&kPSI[buf][s4]);
+                            const f32x4 zk4 = FAST ? *reinterpret_cast<const f32x4 *>(&Aw[w][s4])
+                                                   : *reinterpret_cast<const f32x4 *>(&kSUFL[buf][s4]);
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const int j = 4 * jq + e;
-                            const float x = fminf(sp4[e], Y - psi4[e]);   // min(SUF_s, MID, PRE_t) - psi_s
-                            const float xm = fminf(x, 0.f);
-                            float P = fexp2(fmaf(S[0][j], p.sc2, fmaf(betal, xm, -lse)));
-                            if (!full) P = t_valid ? P : 0.f;
-                            const float dS = P * (dP[0][j] - del);
-                            const float gg = (x <= 0.f) ? dS : 0.f;
-                            racc = fmaf(gg, frcp(fexp2(sfl4[e] - ct) + mterm), racc);
-                            S[0][j] = dS;
+                            for (int e = 0; e < 4; ++e) {
+                                const int j = 4 * jq + e;
+                                const float x = fminf(sp4[e], Y - psi4[e]);  // min(SUF_s, MID, PRE_t) - psi_s
+                                const float xm = fminf(x, 0.f);
+                                float P = fexp2(fmaf(S[0][j], p.sc2, fmaf(betal, xm, -lse)));
+                                if (!full) P = t_valid ? P : 0.f;
+                                const float dS = P * (dP[0][j] - del);
+                                const float gg = (x <= 0.f) ? dS : 0.f;
+                                if constexpr (FAST)
+                                    rblk = fmaf(gg, frcp(zk4[e] + bq), rblk);
+                                else
+                                    racc = fmaf(gg, frcp(fexp2(zk4[e] - ct) + mterm), racc);
+                                S[0][j] = dS;
+                            }
                         }
-                    }
+                    };
+#if FPA_Q_FAST
+                    if (fast)
+                        offdiag(std::true_type{});
+                    else
+#endif
+                        offdiag(std::false_type{});
                 } else {
 #pragma unroll
                     for (int jq = 0; jq < 4; ++jq) {
@@ -166,6 +209,7 @@ fpa_bwd_q_kernel(BwdParams p) {
                 for (int dt = 0; dt < NDT; ++dt)
                     dqacc[dt] = mma_p2_p3<T, 1, true>(dqacc[dt], S, Kt + 32 * mt * PK, PK, 32 * dt, lane);
             }
+            if (fast) racc = fmaf(fexp2(ct - R), rblk, racc);  // R_t gets 2^{c_t} sum g / Z
         }
         if (jb > 0) lstore(buf ^ 1);
         __syncthreads();
@@ -198,7 +242,7 @@ fpa_bwd_q_kernel(BwdParams p) {
 template <typename T, int D>
 static hipError_t launch_q_t(const BwdParams &p, hipStream_t s) {
     const int nqt = (p.T + 127) / 128;
-    constexpr int WPE = (D >= 128) ? 1 : 2;
+    constexpr int WPE = (D >= 128) ? 1 : FPA_Q_WPE;
     hipLaunchKernelGGL((fpa_bwd_q_kernel<T, D, WPE>), dim3(nqt, p.BH), dim3(NTHREADS), 0, s, p);
     return hipGetLastError();
 }

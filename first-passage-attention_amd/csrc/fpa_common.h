@@ -58,6 +58,14 @@ __device__ __forceinline__ float lse2_pair(float a, float b) {
 // Element (row, column) of accumulator register j for lane group g (column = lane % 32).
 __device__ __forceinline__ constexpr int acc_row(int j, int g) { return 8 * (j / 4) + 4 * g + (j % 4); }
 
+__device__ __forceinline__ float uniform_f(float x) {  // value of the first active lane
+    return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x)));
+}
+
+// A tile of soft-min terms whose exponents span less than this many binades uses one shared
+// reference (products of per-key and per-query factors); wider tiles use per-element references.
+constexpr float FAST_SPREAD = 96.f;
+
 __device__ __forceinline__ f32x16 zero16() {
     f32x16 z;
 #pragma unroll
@@ -143,6 +151,26 @@ __device__ __forceinline__ f32x16 mma_p1_lds_reg(f32x16 acc, const T *arow, int 
             acc = MT<T>::mma(a[1], breg[4 * i + 1], acc);
             acc = MT<T>::mma(a[2], breg[4 * i + 2], acc);
             acc = MT<T>::mma(a[3], breg[4 * i + 3], acc);
+        }
+    }
+    return acc;
+}
+
+// acc += A * B over a contraction of length K, both operands P1 rows in LDS.
+template <typename T, int K>
+__device__ __forceinline__ f32x16 mma_p1_lds_lds(f32x16 acc, const T *arow, const T *brow, int g) {
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+        for (int i = 0; i < K / 16; ++i)
+            acc = MT<T>::mma(*reinterpret_cast<const h8 *>(arow + 16 * i + 8 * g),
+                             *reinterpret_cast<const h8 *>(brow + 16 * i + 8 * g), acc);
+    } else {
+#pragma unroll
+        for (int i = 0; i < K / 8; ++i) {
+            const f32x4 a = *reinterpret_cast<const f32x4 *>(arow + g * (K / 2) + 4 * i);
+            const f32x4 b = *reinterpret_cast<const f32x4 *>(brow + g * (K / 2) + 4 * i);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc = MT<T>::mma(a[e], b[e], acc);
         }
     }
     return acc;
@@ -250,6 +278,108 @@ __device__ __forceinline__ void diag_x_queries(float (&X)[16], float &r, const f
 }
 
 // ---------------------------------------------------------------------------
+// Swizzled LDS tiles filled by direct global -> LDS loads.
+//
+// A tile of NR rows x D elements is stored unpadded (D * sizeof(T) bytes per row) in
+// 16-byte chunks; logical chunk lc of row r sits at physical chunk lc ^ (r & SW), which
+// spreads a column of chunks over the LDS banks.  global_load_lds_dwordx4 writes the 16
+// bytes of lane l of a wave to (LDS base + 16 * l): each wave instruction fills 64
+// consecutive slots, and each lane picks the global row/chunk that belongs in its slot.
+// Rows at or past T are loaded from row T - 1 (finite values that callers mask).
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void gbl_void_t;
+
+template <typename T, int D> struct Sw {
+    static constexpr int CE = 16 / sizeof(T);           // elements per chunk
+    static constexpr int CPR = D / CE;                   // chunks per row
+    static constexpr int SW = (CPR < 8 ? CPR : 8) - 1;   // swizzle mask
+    static constexpr int ROWB = D * sizeof(T);           // bytes per row
+    // byte offset of element e (a multiple of 4 elements for fp16) of row r
+    __device__ static __forceinline__ int off(int r, int e) {
+        return r * ROWB + (((e / CE) ^ (r & SW)) << 4) + (e % CE) * (int)sizeof(T);
+    }
+    template <int NR> static constexpr int bytes() { return NR * ROWB; }
+};
+
+__device__ __forceinline__ void gl_lds16(const void *src, void *lds_dst) {
+    __builtin_amdgcn_global_load_lds((gbl_void_t *)(src), (lds_void_t *)(lds_dst), 16, 0, 0);
+}
+
+// Issue the loads of rows [row0, row0 + NR) of a (B, H, T, D)-strided tensor into the swizzled
+// tile at `tile` (all waves of the workgroup take part; completes at the next vmcnt(0) wait).
+template <typename T, int D, int NR>
+__device__ __forceinline__ void tile_issue(char *tile, const T *base, int64_t st, int row0, int T_, int wave, int lane) {
+    using S = Sw<T, D>;
+    constexpr int NI = NR * S::CPR / 64;  // wave instructions per tile
+    static_assert(NR * S::CPR % 64 == 0, "tile must fill whole wave instructions");
+    for (int i = wave; i < NI; i += NTHREADS / 64) {
+        const int k = 64 * i + lane;
+        const int r = k / S::CPR, pc = k % S::CPR, lc = pc ^ (r & S::SW);
+        const int row = min(row0 + r, T_ - 1);
+        gl_lds16(base + (int64_t)row * st + lc * S::CE, tile + 1024 * i);
+    }
+}
+
+// Load n consecutive floats (n <= 256, multiple of 4) from global into LDS with one wave.
+__device__ __forceinline__ void vec_issue(float *lds, const float *src, int n, int lane) {
+    if (4 * lane < n) gl_lds16(src + 4 * lane, lds);
+}
+
+__device__ __forceinline__ void wait_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// P1 operands from a swizzled tile row.
+template <typename T, int K>
+__device__ __forceinline__ f32x16 mma_p1_sw_reg(f32x16 acc, const char *tile, int row, int g, const OpRow<T, K> &breg) {
+    using S = Sw<T, K>;
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+        for (int i = 0; i < K / 16; ++i)
+            acc = MT<T>::mma(*reinterpret_cast<const h8 *>(tile + S::off(row, 16 * i + 8 * g)), breg[i], acc);
+    } else {
+#pragma unroll
+        for (int i = 0; i < K / 8; ++i) {
+            const f32x4 a = *reinterpret_cast<const f32x4 *>(tile + S::off(row, g * (K / 2) + 4 * i));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc = MT<T>::mma(a[e], breg[4 * i + e], acc);
+        }
+    }
+    return acc;
+}
+
+// acc += A * B with the P3 operand from a swizzled tile (rows = contraction, column n = ncol0 + c)
+// and the P2 operand from the accumulator tile c0 (rows 32*mt0 .. of the tile are its rows).
+template <typename T, int D, bool A_IS_P3>
+__device__ __forceinline__ f32x16 mma_p2_p3_sw(f32x16 acc, const f32x16 &c0, const char *tile, int row0, int ncol0,
+                                               int lane) {
+    using S = Sw<T, D>;
+    const int g = lane >> 5;
+    if constexpr (sizeof(T) == 2) {
+        const int j = lane & 15, q = lane >> 4;
+        const int col = ncol0 + 16 * (q & 1) + 4 * (j & 3);
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            h8 p2;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) p2[e] = (f16)c0[8 * hf + e];
+            const int row = row0 + 16 * hf + 4 * (q >> 1) + (j >> 2);
+            const h4 lo = ds_read_tr16(reinterpret_cast<const f16 *>(tile + S::off(row, col)));
+            const h4 hi = ds_read_tr16(reinterpret_cast<const f16 *>(tile + S::off(row + 8, col)));
+            const h8 p3 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            acc = A_IS_P3 ? MT<T>::mma(p3, p2, acc) : MT<T>::mma(p2, p3, acc);
+        }
+    } else {
+        const int n = ncol0 + (lane & 31);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const float p3 = *reinterpret_cast<const float *>(tile + S::off(row0 + acc_row(j, g), n));
+            acc = A_IS_P3 ? MT<T>::mma(p3, c0[j], acc) : MT<T>::mma(c0[j], p3, acc);
+        }
+    }
+    return acc;
+}
+
+// ---------------------------------------------------------------------------
 // Register prefetch of an NR x D tile of a (B, H, T, D)-strided tensor (rows row0 + r,
 // zero past T), stored afterwards into a natural-layout LDS tile of the given pitch.
 // ---------------------------------------------------------------------------
@@ -325,11 +455,12 @@ __device__ __forceinline__ float wave_sum(float x) {
 // State planes (float offsets), each plane is BH * TP floats except the two block planes.
 struct StateLayout {
     int64_t BH, TP, NB;
-    __host__ __device__ int64_t plane(int k) const { return (int64_t)k * BH * TP; }  // 0..5
-    __host__ __device__ int64_t bplane(int k) const { return 6 * BH * TP + (int64_t)k * BH * NB; }  // 0..1
-    __host__ __device__ int64_t total() const { return 6 * BH * TP + 2 * BH * NB; }
+    __host__ __device__ int64_t plane(int k) const { return (int64_t)k * BH * TP; }  // 0..7
+    __host__ __device__ int64_t bplane(int k) const { return 8 * BH * TP + (int64_t)k * BH * NB; }  // 0..1
+    __host__ __device__ int64_t total() const { return 8 * BH * TP + 2 * BH * NB; }
 };
-enum { PL_PHI = 0, PL_PSI = 1, PL_PRE = 2, PL_PREL = 3, PL_SUF = 4, PL_SUFL = 5 };
+// PL_CA = beta*log2e*min(SUF - psi, 0) and PL_CP = beta*log2e*psi: the forward's per-key bias terms.
+enum { PL_PHI = 0, PL_PSI = 1, PL_PRE = 2, PL_PREL = 3, PL_SUF = 4, PL_SUFL = 5, PL_CA = 6, PL_CP = 7 };
 enum { BP_MIN = 0, BP_LSE = 1 };
 
 }  // namespace fpa

@@ -13,6 +13,11 @@
 #include "fpa_common.h"
 #include "fpa_params.h"
 
+// Tuning knob (build-time): waves per SIMD of the D <= 64 forward kernel.
+#ifndef FPA_FWD_WPE
+#define FPA_FWD_WPE 2
+#endif
+
 namespace fpa {
 
 // ---------------------------------------------------------------------------
@@ -21,6 +26,7 @@ namespace fpa {
 //   PRE_t     = min phi[sb .. t]           PREL_t = log2 sum 2^a[sb .. t]
 //   SUF_s     = min phi(s .. eb)           SUFL_s = log2 sum 2^a(s .. eb)
 //   BMIN, BLSE: the whole block.           a_u = -phi_u * log2(e) / tau
+//   CA, CP    : beta*log2e*min(SUF - psi, 0) and beta*log2e*psi (the forward's per-key terms)
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(64) fpa_stats_kernel(StatsParams p) {
     const int blk = blockIdx.x, bh = blockIdx.y;
@@ -67,6 +73,9 @@ __global__ void __launch_bounds__(64) fpa_stats_kernel(StatsParams p) {
     p.state[L.plane(PL_PREL) + r] = pl;
     p.state[L.plane(PL_SUF) + r] = suf;
     p.state[L.plane(PL_SUFL) + r] = sufl;
+    const float betal = p.beta[bh % p.H] * LOG2E;
+    p.state[L.plane(PL_CA) + r] = betal * fminf(suf - ps, 0.f);
+    p.state[L.plane(PL_CP) + r] = betal * ps;
     if (lane == 63) {
         p.state[L.bplane(BP_MIN) + (int64_t)bh * p.NB + blk] = pm;
         p.state[L.bplane(BP_LSE) + (int64_t)bh * p.NB + blk] = pl;
@@ -278,7 +287,7 @@ fpa_fwd_kernel(FwdParams p) {
 template <typename T, int D>
 static hipError_t launch_fwd_t(const FwdParams &p, hipStream_t s) {
     const int nqt = (p.T + 127) / 128;
-    constexpr int WPE = (D >= 128) ? 1 : 2;
+    constexpr int WPE = (D >= 128) ? 1 : FPA_FWD_WPE;
     hipLaunchKernelGGL((fpa_fwd_kernel<T, D, WPE>), dim3(nqt, p.BH), dim3(NTHREADS), 0, s, p);
     return hipGetLastError();
 }

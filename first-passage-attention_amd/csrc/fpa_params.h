@@ -14,6 +14,7 @@ struct S3 {
 struct StatsParams {
     const float *phi; S3 sphi;
     const float *psi; S3 spsi;
+    const float *beta;
     float *state;
     int H, T, TP, NB, BH;
     float il2;  // log2(e) / tau
@@ -66,7 +67,6 @@ hipError_t launch_bwd_prep(const BwdParams &p, int dtype, int D, hipStream_t s);
 hipError_t launch_bwd_kv(const BwdParams &p, int dtype, int D, hipStream_t s);
 hipError_t launch_bwd_q(const BwdParams &p, int dtype, int D, hipStream_t s);
 hipError_t launch_bwd_combine(const BwdParams &p, hipStream_t s);
-hipError_t launch_bwd_dbeta(const BwdParams &p, hipStream_t s);
 
 // Head dimensions with built kernels.
 inline bool supported_d(int dtype, int D) {

@@ -13,7 +13,8 @@
  *               _stats / _fwd Triton kernels (83-100, 103-162);
  *   fpa_bwd  <- _FirstPassageAttention.backward (kernel.py:424-451) with the
  *               _bwd_delta/_bwd_kv/_bwd_dphi_diag/_bwd_q/_bwd_dphi kernels
- *               (165-370) and the dbeta sum at kernel.py:450;
+ *               (165-370) and the dbeta sum at kernel.py:450 (four kernels here:
+ *               delta, key side, query side, phi/beta combine);
  *   fpa_state_floats / fpa_bwd_workspace_bytes <- the scratch allocations of
  *               kernel.py:390-392, 406-407, 430-436, sized so the caller owns them.
  * Error behaviour mirrors the validation of first_passage_attention
@@ -39,8 +40,8 @@ extern "C" {
 #define FPA_BWD_DELTA 1    /* Delta_t = sum_d dO o                         */
 #define FPA_BWD_KEYS 2     /* key side: dk, dv, dpsi, dbeta partials, ...  */
 #define FPA_BWD_QUERIES 4  /* query side: dq, query-block soft-min sums    */
-#define FPA_BWD_PHI 8      /* dphi                                         */
-#define FPA_BWD_BETA 16    /* dbeta                                        */
+#define FPA_BWD_PHI 8      /* dphi and dbeta (one kernel)                  */
+#define FPA_BWD_BETA 16    /* same kernel as FPA_BWD_PHI                   */
 
 /* status codes */
 #define FPA_OK 0
