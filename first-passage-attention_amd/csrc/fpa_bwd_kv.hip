@@ -69,7 +69,7 @@ fpa_bwd_kv_kernel(BwdParams p) {
     __shared__ __attribute__((aligned(16))) T Qs[2 * TS + (DT - D)];
     __shared__ __attribute__((aligned(16))) T dOs[2 * TS + (DT - D)];
     __shared__ __attribute__((aligned(16))) float rLSE[2][BQ], rDEL[2][BQ], rPRE[2][BQ], rPREL[2][BQ];
-    __shared__ float kPHI[BK];
+    __shared__ __attribute__((aligned(16))) float kPHI[BK];
     __shared__ __attribute__((aligned(16))) float Bw[4][BQ];  // per-wave query factors of the shared-reference path
 
     const int tid = threadIdx.x, lane = tid % 64, g = lane / 32, c = lane % 32;
@@ -279,8 +279,8 @@ fpa_bwd_kv_kernel(BwdParams p) {
     }
 
     // Per-key outputs (lanes c and c + 32 hold the same key, different queries).
-    gsum += __shfl_xor(gsum, 32, 64);
-    Wacc += __shfl_xor(Wacc, 32, 64);
+    gsum = sum_halves(gsum);
+    Wacc = sum_halves(Wacc);
     const float dbw = wave_sum(dbacc);
     if (lane == 0) p.dbp[((int64_t)bh * p.NKV + kt) * 4 + w] = dbw;  // 0 for waves past T
     if (!wave_active) return;

@@ -215,7 +215,7 @@ fpa_bwd_q_kernel(BwdParams p) {
         __syncthreads();
     }
 
-    racc += __shfl_xor(racc, 32, 64);
+    racc = sum_halves(racc);
     if (!wave_active) return;
     if (g == 0 && tq < p.TP) p.rsum[rowbase + tq] = t_valid ? racc : 0.f;
     if (!t_valid) return;

@@ -244,13 +244,23 @@ __device__ __forceinline__ f32x16 mma_p2_p3(f32x16 acc, const f32x16 (&c)[NT], c
 // ---------------------------------------------------------------------------
 
 // Lane = query tr (0..63 in the block); registers = keys 32*mt + acc_row(j, g).  Descending
-// scan; `r` carries min phi[32*mt + 33 .. tr] in and min phi[32*mt + 1 .. tr] out.
+// scan; `r` carries min phi[32*mt + 33 .. tr] in and min phi[32*mt + 1 .. tr] out.  `phi` is
+// the block's 64 values in LDS (16-byte aligned): every read is unconditional (the same
+// address in all lanes) and positions past tr are masked by a select, so the scan has no
+// branches.
 __device__ __forceinline__ void diag_x_keys(float (&X)[16], float &r, const float *phi, int mt, int tr, int g) {
+    float pv[33];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const f32x4 v = *reinterpret_cast<const f32x4 *>(phi + 32 * mt + 4 * i);
+        pv[4 * i] = v[0]; pv[4 * i + 1] = v[1]; pv[4 * i + 2] = v[2]; pv[4 * i + 3] = v[3];
+    }
+    pv[32] = (mt == 0) ? phi[32] : pinf();
     float rr[33];
 #pragma unroll
     for (int k = 32; k >= 1; --k) {
         const int u = 32 * mt + k;
-        if (u < G) r = fminf(r, (u <= tr) ? phi[u] : pinf());
+        r = fminf(r, (u <= tr) ? pv[k] : pinf());
         rr[k] = r;  // min phi[u .. tr]: the value for key u - 1
     }
 #pragma unroll
@@ -262,12 +272,19 @@ __device__ __forceinline__ void diag_x_keys(float (&X)[16], float &r, const floa
 
 // Lane = key sr (0..63 in the block); registers = queries 32*mt + acc_row(j, g).  Ascending
 // scan; `r` carries min phi[sr+1 .. 32*mt - 1] in and min phi[sr+1 .. 32*mt + 31] out.
+// Branch-free like diag_x_keys.
 __device__ __forceinline__ void diag_x_queries(float (&X)[16], float &r, const float *phi, int mt, int sr, int g) {
+    float pv[32];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const f32x4 v = *reinterpret_cast<const f32x4 *>(phi + 32 * mt + 4 * i);
+        pv[4 * i] = v[0]; pv[4 * i + 1] = v[1]; pv[4 * i + 2] = v[2]; pv[4 * i + 3] = v[3];
+    }
     float rr[32];
 #pragma unroll
     for (int k = 0; k < 32; ++k) {
         const int u = 32 * mt + k;
-        r = fminf(r, (u > sr) ? phi[u] : pinf());
+        r = fminf(r, (u > sr) ? pv[k] : pinf());
         rr[k] = r;  // min phi[sr+1 .. u]: the value for query u
     }
 #pragma unroll
@@ -275,6 +292,16 @@ __device__ __forceinline__ void diag_x_queries(float (&X)[16], float &r, const f
         const int k0 = 8 * (j / 4) + (j % 4);
         X[j] = g ? rr[k0 + 4] : rr[k0];
     }
+}
+
+// x[l] + x[l ^ 32] and max(x[l], x[l ^ 32]) with the gfx950 half-wave swap (no LDS round trip).
+__device__ __forceinline__ float sum_halves(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float max_halves(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 // ---------------------------------------------------------------------------

@@ -211,12 +211,17 @@ fpa_fwd_kernel(FwdParams p) {
 #pragma unroll
                 for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-                    for (int j = 0; j < 16; ++j) {
-                        const int sr = 32 * mt + acc_row(j, g);
-                        const float b2 = (sr < tr) ? __builtin_amdgcn_fmed3f(0.f, fmaf(betal, X[mt][j], -cP[buf][sr]), E)
-                                                   : 0.f;  // b_tt = 0
-                        const float z = fmaf(s[mt][j], p.sc2, b2);
-                        s[mt][j] = (sr > tr || s0 + sr >= p.T) ? ninf() : z;
+                    for (int jq = 0; jq < 4; ++jq) {
+                        const int s4 = 32 * mt + 8 * jq + 4 * g;
+                        const f32x4 p4 = *reinterpret_cast<const f32x4 *>(&cP[buf][s4]);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int j = 4 * jq + e, sr = s4 + e;
+                            const float bx = __builtin_amdgcn_fmed3f(0.f, fmaf(betal, X[mt][j], -p4[e]), E);
+                            const float b2 = (sr < tr) ? bx : 0.f;  // b_tt = 0
+                            const float z = fmaf(s[mt][j], p.sc2, b2);
+                            s[mt][j] = (sr > tr || s0 + sr >= p.T) ? ninf() : z;
+                        }
                     }
             }
 
@@ -226,7 +231,7 @@ fpa_fwd_kernel(FwdParams p) {
             for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
                 for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[mt][j]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            mx = max_halves(mx);
             if (__any(mx > m_i + RESCALE_SLACK)) {
                 const float m_new = fmaxf(m_i, mx);
                 const float alpha = fexp2(m_i - m_new);  // 0 on the first tile (m_i = -inf)
@@ -246,7 +251,7 @@ fpa_fwd_kernel(FwdParams p) {
                     s[mt][j] = pv;
                     rs += pv;
                 }
-            l_i += rs + __shfl_xor(rs, 32, 64);
+            l_i += sum_halves(rs);
 
             // O^T[d][t] += V^T[d][s] P^T[s][t]   (V read transposed from its natural layout)
             const T *Vt = Vs + buf * TS;
