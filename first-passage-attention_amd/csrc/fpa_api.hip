@@ -26,19 +26,19 @@ int64_t tp_of(int64_t T) { return ((T + G - 1) / G) * G; }
 int64_t align64(int64_t n) { return (n + 63) / 64 * 64; }  // floats -> 256-byte multiple
 
 struct WsLayout {
-    int64_t delta, wsum, rsum, gd, tbuf, dbp, total;  // float offsets
+    int64_t qinfo, wsum, rsum, gd, tbuf, dbp, total;  // float offsets
 };
 
 WsLayout ws_layout(int64_t B, int64_t H, int64_t T) {
-    const int64_t BH = B * H, TP = tp_of(T), NB = TP / G, NKV = (T + 127) / 128;
+    const int64_t BH = B * H, TP = tp_of(T), NB = TP / G, NK32 = (T + 31) / 32;
     WsLayout w;
     int64_t off = 0;
-    w.delta = off; off += align64(BH * TP);
+    w.qinfo = off; off += align64(QI_N * BH * TP);
     w.wsum = off;  off += align64(BH * TP);
     w.rsum = off;  off += align64(BH * TP);
     w.gd = off;    off += align64(BH * NB * G * G);
     w.tbuf = off;  off += align64(BH * NB * NB * 2);
-    w.dbp = off;   off += align64(BH * NKV * 4);
+    w.dbp = off;   off += align64(BH * NK32);
     w.total = off;
     return w;
 }
@@ -66,6 +66,9 @@ int check_rows(const void *ptr, const int64_t *st, int32_t dtype, const char *na
     if ((reinterpret_cast<uintptr_t>(ptr) & 15) != 0 || st[0] % ce || st[1] % ce || st[2] % ce)
         return fail(FPA_ERR_INVALID, std::string(name) +
                                          " rows must be 16-byte aligned (contiguous head dimension, aligned strides)");
+    // Tile loads address 64 rows with 32-bit byte offsets from the first row.
+    if (st[2] < 0 || st[2] * 64 * (ce == 8 ? 2 : 4) >= (int64_t(1) << 31))
+        return fail(FPA_ERR_INVALID, std::string(name) + " row stride is out of range (at most 2^25 bytes)");
     return FPA_OK;
 }
 
@@ -163,10 +166,11 @@ int fpa_bwd(const FpaBwdArgs *a, void *stream) {
     p.dv = a->dv; p.sdv = s3(a->sdv);
     p.beta = a->beta; p.lse = a->lse; p.state = a->state;
     p.dphi = a->dphi; p.dpsi = a->dpsi; p.dbeta = a->dbeta;
-    p.delta = ws + wl.delta; p.wsum = ws + wl.wsum; p.rsum = ws + wl.rsum;
+    p.qinfo = ws + wl.qinfo; p.delta = p.qinfo + QI_DEL * (a->B * a->H) * TP;
+    p.wsum = ws + wl.wsum; p.rsum = ws + wl.rsum;
     p.gd = ws + wl.gd; p.tbuf = ws + wl.tbuf; p.dbp = ws + wl.dbp;
     p.B = (int)a->B; p.H = (int)a->H; p.T = (int)a->T; p.TP = (int)TP; p.NB = (int)(TP / G);
-    p.BH = (int)(a->B * a->H); p.NKV = (int)((a->T + 127) / 128);
+    p.BH = (int)(a->B * a->H); p.NK32 = (int)((a->T + 31) / 32);
     p.sc2 = LOG2E / sqrtf((float)a->D);
     p.smscale = 1.0f / sqrtf((float)a->D);
     p.il2 = LOG2E / a->tau;

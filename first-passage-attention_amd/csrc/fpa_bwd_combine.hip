@@ -59,10 +59,10 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
     const int NB = p.NB;
 
     if (U == 0 && b == 0) {  // dbeta[h] = sum over batches and key-side partials
-        const int n = p.NKV * 4;
+        const int n = p.NK32;
         float acc = 0.f;
         for (int bb = 0; bb < p.B; ++bb) {
-            const float *src = p.dbp + ((int64_t)(bb * p.H + h) * p.NKV) * 4;
+            const float *src = p.dbp + (int64_t)(bb * p.H + h) * p.NK32;
             for (int i = tid; i < n; i += NTHREADS) acc += src[i];
         }
         const float tot = block_sum_256(acc, red);

@@ -1,10 +1,10 @@
 // fpa_bwd_kv.hip -- key-side backward of First Passage Attention.
 //
 // Reference behaviour: _bwd_delta (kernel.py:165-174) and _bwd_kv (kernel.py:177-265)
-// of yliu-fort/first-passage-attention.  gfx950 design: a workgroup of 4 waves owns
-// 128 keys (32 per wave, one key per lane column) and streams 64-query blocks from
-// the diagonal to T through double-buffered LDS (register prefetch of the next block,
-// one barrier per block).  Each wave computes S = Q K^T and dP = dO V^T with K, V
+// of yliu-fort/first-passage-attention.  gfx950 design: a workgroup of FPA_NW waves owns
+// 32 keys per wave (one key per lane column) and streams 64-query blocks from the
+// diagonal to T through double-buffered, padded LDS tiles filled by direct global->LDS
+// loads (one barrier per block).  Each wave computes S = Q K^T and dP = dO V^T with K, V
 // held in registers, then dV^T += dO^T P and dK^T += Q^T dS on the 32x32 MFMA (dO^T
 // and Q^T read from the row-major tiles with LDS transpose reads).  Per key it reduces
 //   dpsi_s  = -beta * sum_t g_ts                       (g = [x <= 0] dS, strict t > s)
@@ -22,13 +22,20 @@
 #ifndef FPA_KV_WPE
 #define FPA_KV_WPE 2
 #endif
-#ifndef FPA_KV_FAST
-#define FPA_KV_FAST 0
+#ifndef FPA_KV_PROD
+#define FPA_KV_PROD 1
 #endif
 
 namespace fpa {
 
-// Delta_t = sum_d dO_td O_td (fp32), zero for padded rows.
+// Per-query planes of the backward (QI_*), for t < TP:
+//   LSE   lse_t (+inf past T: P = 0 there with no per-element mask)
+//   DEL   Delta_t = sum_d dO_td O_td (0 past T)
+//   PRE   PRE_t (+inf past T)
+//   ZQ    with PRL_t = PREL_t - BLSE <= 0 (BLSE = log2 sum 2^a over t's block; 0 past T):
+//         2^{PRL_t} > 0 when the block's spread -PRL_{first row} is at most PROD_SPREAD
+//         (product form of the soft-min denominators), else PRL_t <= 0 (exact form).  The sign
+//         of the block's first entry tells the two apart.
 template <typename T, int D>
 __global__ void __launch_bounds__(NTHREADS) fpa_bwd_prep_kernel(BwdParams p) {
     constexpr int CE = MT<T>::CHUNK;
@@ -55,22 +62,32 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_prep_kernel(BwdParams p) {
     }
     acc += __shfl_xor(acc, 1, 64);
     acc += __shfl_xor(acc, 2, 64);
-    if (part == 0 && row < p.TP) p.delta[(int64_t)bh * p.TP + row] = acc;
+    if (part == 0 && row < p.TP) {
+        const StateLayout L{p.BH, p.TP, p.NB};
+        const int64_t r = (int64_t)bh * p.TP + row, QP = (int64_t)p.BH * p.TP;
+        const bool ok = row < p.T;
+        const float blse = p.state[L.bplane(BP_LSE) + (int64_t)bh * p.NB + row / G];
+        const float prl = ok ? p.state[L.plane(PL_PREL) + r] - blse : 0.f;
+        const float spread = blse - p.state[L.plane(PL_PREL) + (int64_t)bh * p.TP + (row / G) * G];
+        p.qinfo[QI_LSE * QP + r] = ok ? p.lse[r] : pinf();
+        p.qinfo[QI_DEL * QP + r] = ok ? acc : 0.f;
+        p.qinfo[QI_PRE * QP + r] = ok ? p.state[L.plane(PL_PRE) + r] : pinf();
+        p.qinfo[QI_ZQ * QP + r] = (FPA_KV_PROD && spread <= PROD_SPREAD) ? fexp2(prl) : prl;
+    }
 }
 
-template <typename T, int D, int WPE>
-__global__ void __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+template <typename T, int D, int WPE, int NW>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 fpa_bwd_kv_kernel(BwdParams p) {
-    constexpr int BK = 128, BQ = 64;   // keys per workgroup, queries per iteration (one block)
+    constexpr int BK = 32 * NW, BQ = 64;   // keys per workgroup, queries per iteration (one block)
     constexpr int DT = D < 32 ? 32 : D;
     constexpr int NDT = DT / 32;
-    constexpr int PQ = D + (sizeof(T) == 2 ? 8 : 4);  // tile pitch (elements)
-    constexpr int TS = BQ * PQ;
-    __shared__ __attribute__((aligned(16))) T Qs[2 * TS + (DT - D)];
-    __shared__ __attribute__((aligned(16))) T dOs[2 * TS + (DT - D)];
-    __shared__ __attribute__((aligned(16))) float rLSE[2][BQ], rDEL[2][BQ], rPRE[2][BQ], rPREL[2][BQ];
+    constexpr int TB = Pad<T, DT>::template bytes<BQ>();  // one padded Q or dO tile
+    __shared__ __attribute__((aligned(1024))) char Qs[2][TB];
+    __shared__ __attribute__((aligned(1024))) char dOs[2][TB];
+    // Per-query planes of a block: QI_LSE, QI_DEL, QI_PRE, QI_ZQ.
+    __shared__ __attribute__((aligned(1024))) float qi[2][QI_N][BQ];
     __shared__ __attribute__((aligned(16))) float kPHI[BK];
-    __shared__ __attribute__((aligned(16))) float Bw[4][BQ];  // per-wave query factors of the shared-reference path
 
     const int tid = threadIdx.x, lane = tid % 64, g = lane / 32, c = lane % 32;
     const int w = __builtin_amdgcn_readfirstlane(tid / 64);  // wave index, uniform across the wave
@@ -85,11 +102,25 @@ fpa_bwd_kv_kernel(BwdParams p) {
     const StateLayout L{p.BH, p.TP, p.NB};
     const int64_t rowbase = (int64_t)bh * p.TP;
     const int64_t brow = (int64_t)bh * p.NB;
+    const int64_t QP = (int64_t)p.BH * p.TP;
 
     const T *Qb = static_cast<const T *>(p.q) + b * p.sq.b + h * p.sq.h;
     const T *Kb = static_cast<const T *>(p.k) + b * p.sk.b + h * p.sk.h;
     const T *Vb = static_cast<const T *>(p.v) + b * p.sv.b + h * p.sv.h;
     const T *DOb = static_cast<const T *>(p.dout) + b * p.sdo.b + h * p.sdo.h;
+    // lanes 0-15: LSE, 16-31: DEL, 32-47: PRE, 48-63: ZQ
+    const float *qi_src = p.qinfo + (lane >> 4) * QP + rowbase + 4 * (lane & 15);
+
+    TileLoader<T, D, DT, BQ, NW> qld, dld;
+    qld.init(p.sq.t, w, lane);
+    dld.init(p.sdo.t, w, lane);
+    auto issue = [&](int ib, int buf) {
+        qld.issue(Qs[buf], Qb, p.sq.t, ib * BQ, p.T, w, lane);
+        dld.issue(dOs[buf], DOb, p.sdo.t, ib * BQ, p.T, w, lane);
+        if (w == NW - 1) gl_lds16(qi_src + ib * BQ, &qi[buf][0][0]);
+    };
+    const int ib0 = k0 / G;
+    issue(ib0, 0);
 
     OpRow<T, D> kreg, vreg;
     load_row_p1<T, D>(kreg, Kb + (int64_t)s * p.sk.t, s_valid, g);
@@ -104,13 +135,6 @@ fpa_bwd_kv_kernel(BwdParams p) {
     }
     const float Cs = (suf < pinf()) ? -suf * p.il2 : ninf();  // max a over (s, end of block)
     const float sufpsi = suf - psi_s;
-
-    if constexpr (D < DT) {  // columns D..31 read by the padded transpose reads stay zero
-        for (int i = tid; i < 2 * TS + (DT - D); i += NTHREADS) {
-            Qs[i] = (T)0.f;
-            dOs[i] = (T)0.f;
-        }
-    }
     if (tid < BK) kPHI[tid] = (k0 + tid < p.TP) ? p.state[L.plane(PL_PHI) + rowbase + k0 + tid] : pinf();
 
     f32x16 dkacc[NDT], dvacc[NDT];
@@ -123,40 +147,21 @@ fpa_bwd_kv_kernel(BwdParams p) {
     float mid = pinf(), midl = ninf(), cmid = ninf();  // over blocks strictly between jb and ib
     const float *phiblk = kPHI + (sb - k0);
 
-    TileRegs<T, D, BQ> qr, dor;
-    float pf_lse = 0.f, pf_del = 0.f, pf_pre = 0.f, pf_prel = 0.f;
-    auto gload = [&](int ib) {
-        qr.load(Qb, p.sq.t, ib * BQ, p.T);
-        dor.load(DOb, p.sdo.t, ib * BQ, p.T);
-        if (tid < BQ) {
-            const int64_t r = rowbase + ib * BQ + tid;
-            pf_lse = p.lse[r];
-            pf_del = p.delta[r];
-            pf_pre = p.state[L.plane(PL_PRE) + r];
-            pf_prel = p.state[L.plane(PL_PREL) + r];
-        }
-    };
-    auto lstore = [&](int buf) {
-        qr.store(Qs + buf * TS, PQ);
-        dor.store(dOs + buf * TS, PQ);
-        if (tid < BQ) {
-            rLSE[buf][tid] = pf_lse;
-            rDEL[buf][tid] = pf_del;
-            rPRE[buf][tid] = pf_pre;
-            rPREL[buf][tid] = pf_prel;
-        }
-    };
-
-    const int ib0 = k0 / G;
-    gload(ib0);
-    lstore(0);
+    wait_loads();
     __syncthreads();
     for (int ib = ib0, it = 0; ib < p.NB; ++ib, ++it) {
         const int buf = it & 1;
-        if (ib + 1 < p.NB) gload(ib + 1);
+        if (ib + 1 < p.NB) issue(ib + 1, buf ^ 1);
         if (wave_active && ib >= jb) {
-            float rs = ninf(), sv = 0.f;
-            bool fast = false;
+            // Soft-min denominators off the diagonal: Z_ts 2^{-rs} = sv + 2^{PREL_t - rs} with the
+            // per-key reference rs = max(C_s, cmid) (sv >= 1 when rs is finite).  With
+            // rsb = rs - BLSE, 2^{PREL_t - rs} = 2^{PRL_t - rsb}; when the block's PRL spread is at
+            // most PROD_SPREAD this is ZQ_t * ck with ZQ_t = 2^{PRL_t} and ck = 2^{min(-rsb, 126)}:
+            // one FMA per element instead of an exp2.  The clamp only changes terms whose
+            // 2^{PREL_t - rs} exceeds 2^{126 - PROD_SPREAD}, where 1/Z is already below 2^{-26} of
+            // the other terms.
+            float rs = ninf(), rsb = ninf(), sv = 0.f, ck = 0.f;
+            bool prod = false;
             if (ib > jb) {
                 if (ib - 1 > jb) {  // block ib - 1 joins the middle
                     const float bm = p.state[L.bplane(BP_MIN) + brow + ib - 1];
@@ -164,97 +169,84 @@ fpa_bwd_kv_kernel(BwdParams p) {
                     midl = lse2_pair(midl, p.state[L.bplane(BP_LSE) + brow + ib - 1]);
                     cmid = fmaxf(cmid, -bm * p.il2);
                 }
-                // Shared reference R >= every exponent of the tile; the smallest pair maximum is
-                // at least max(cmid, a of the block's first query).
-                const float cfirst = uniform_f(Cs);  // lane 0 holds the wave's first key: largest C_s
-                const float R = fmaxf(fmaxf(cfirst, cmid), -p.state[L.bplane(BP_MIN) + brow + ib] * p.il2);
-                const float lo = fmaxf(cmid, -p.state[L.plane(PL_PHI) + rowbase + ib * BQ] * p.il2);
-                fast = FPA_KV_FAST && (R - lo) < FAST_SPREAD;
-                if (fast) {
-                    rs = R;  // W_s and TBUF are scaled by 2^{. - R} at the end of the block
-                    sv = fexp2(sufl - R) + fexp2(midl - R);
-                    Bw[w][lane] = fexp2(rPREL[buf][lane] - R);
-                } else {
-                    rs = fmaxf(Cs, cmid);
-                    sv = (rs > ninf()) ? fexp2(sufl - rs) + fexp2(midl - rs) : 0.f;
-                }
+                rs = fmaxf(Cs, cmid);
+                sv = (rs > ninf()) ? fexp2(sufl - rs) + fexp2(midl - rs) : 0.f;
+                rsb = rs - p.state[L.bplane(BP_LSE) + brow + ib];
+                ck = fexp2(fminf(-rsb, 126.f));
+                prod = uniform_f(qi[buf][QI_ZQ][0]) > 0.f;
             }
             const float Ap = fminf(sufpsi, mid - psi_s);  // min(SUF_s, MID) - psi_s
-            const bool full = (ib + 1) * BQ <= p.T;
-            const T *Qt = Qs + buf * TS;
-            const T *Dt = dOs + buf * TS;
+            const char *Qt = Qs[buf];
+            const char *Dt = dOs[buf];
+            const float *rLSE = qi[buf][QI_LSE], *rDEL = qi[buf][QI_DEL], *rPRE = qi[buf][QI_PRE];
             const bool diag = (ib == jb);
             const int sr = s - sb;
             float r = pinf();  // running min of phi over (s, u] for the in-block scan
             float wblk = 0.f;
 #pragma unroll 1
             for (int mt = 0; mt < 2; ++mt) {
-                f32x16 S[1], dP[1];
-                S[0] = mma_p1_lds_reg<T, D>(zero16(), Qt + (32 * mt + c) * PQ, g, kreg);   // [t][s]
-                dP[0] = mma_p1_lds_reg<T, D>(zero16(), Dt + (32 * mt + c) * PQ, g, vreg);
+                f32x16 S, dP;
+                S = mma_p1_pad_reg<T, D, DT>(zero16(), Qt, 32 * mt + c, g, kreg);   // [t][s]
+                dP = mma_p1_pad_reg<T, D, DT>(zero16(), Dt, 32 * mt + c, g, vreg);
                 float X[16];
                 if (diag) diag_x_queries(X, r, phiblk, mt, sr, g);  // X_ts = min phi(s, t] in the block
                 if (!diag) {
                     // Off the diagonal block every key is valid and every query is later than
-                    // every key; only the rows of a ragged last block are past T.
-                    auto offdiag = [&](auto fast_c) {
-                        constexpr bool FAST = decltype(fast_c)::value;
+                    // every key; rows of a ragged last block are past T and have P = 0.
+                    auto offdiag = [&](auto prod_c) {
+                        constexpr bool PROD = decltype(prod_c)::value;
+                        const float *rZQ = qi[buf][QI_ZQ];
 #pragma unroll
                         for (int jq = 0; jq < 4; ++jq) {
                             const int t4 = 32 * mt + 8 * jq + 4 * g;
-                            const f32x4 lse4 = *reinterpret_cast<const f32x4 *>(&rLSE[buf][t4]);
-                            const f32x4 del4 = *reinterpret_cast<const f32x4 *>(&rDEL[buf][t4]);
-                            const f32x4 pre4 = *reinterpret_cast<const f32x4 *>(&rPRE[buf][t4]);
-                            const f32x4 zq4 = FAST ? *reinterpret_cast<const f32x4 *>(&Bw[w][t4])
-                                                   : *reinterpret_cast<const f32x4 *>(&rPREL[buf][t4]);
+                            const f32x4 lse4 = *reinterpret_cast<const f32x4 *>(&rLSE[t4]);
+                            const f32x4 del4 = *reinterpret_cast<const f32x4 *>(&rDEL[t4]);
+                            const f32x4 pre4 = *reinterpret_cast<const f32x4 *>(&rPRE[t4]);
+                            const f32x4 zq4 = *reinterpret_cast<const f32x4 *>(&rZQ[t4]);
 #pragma unroll
                             for (int e = 0; e < 4; ++e) {
                                 const int j = 4 * jq + e;
                                 const float x = fminf(Ap, pre4[e] - psi_s);  // min(SUF_s, MID, PRE_t) - psi_s
                                 const float xm = fminf(x, 0.f);
-                                float P = fexp2(fmaf(S[0][j], p.sc2, fmaf(betal, xm, -lse4[e])));
-                                if (!full) P = (ib * BQ + t4 + e < p.T) ? P : 0.f;
-                                const float dS = P * (dP[0][j] - del4[e]);
+                                const float P = fexp2(fmaf(S[j], p.sc2, fmaf(betal, xm, -lse4[e])));
+                                const float dS = P * (dP[j] - del4[e]);
                                 const float gg = (x <= 0.f) ? dS : 0.f;
                                 gsum += gg;
-                                dbacc = fmaf(gg, x, dbacc);
-                                // Z_ts 2^{-r} = sv + 2^{PREL_t - r}, r shared (FAST) or per key
-                                const float zq = FAST ? zq4[e] : fexp2(zq4[e] - rs);
-                                wblk = fmaf(gg, frcp(sv + zq), wblk);
-                                S[0][j] = P;
-                                dP[0][j] = dS;
+                                dbacc = fmaf(dS, xm, dbacc);
+                                const float z = PROD ? fmaf(zq4[e], ck, sv) : sv + fexp2(zq4[e] - rsb);
+                                wblk = fmaf(gg, frcp(z), wblk);
+                                S[j] = P;
+                                dP[j] = dS;
                             }
                         }
                     };
-#if FPA_KV_FAST
-                    if (fast)
+                    if (prod)
                         offdiag(std::true_type{});
                     else
-#endif
                         offdiag(std::false_type{});
                 } else {
 #pragma unroll
                     for (int jq = 0; jq < 4; ++jq) {
                         const int t4 = 32 * mt + 8 * jq + 4 * g;
-                        const f32x4 lse4 = *reinterpret_cast<const f32x4 *>(&rLSE[buf][t4]);
-                        const f32x4 del4 = *reinterpret_cast<const f32x4 *>(&rDEL[buf][t4]);
+                        const f32x4 lse4 = *reinterpret_cast<const f32x4 *>(&rLSE[t4]);
+                        const f32x4 del4 = *reinterpret_cast<const f32x4 *>(&rDEL[t4]);
                         f32x4 g4;
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const int j = 4 * jq + e;
                             const int t = ib * BQ + t4 + e;
-                            const bool valid = (t < p.T) && (t >= s) && s_valid;
+                            const bool valid = (t >= s) && s_valid;  // rows past T: lse = +inf gives P = 0
                             const bool strict = valid && (t > s);
                             const float x = X[j] - psi_s;
                             const float xm = strict ? fminf(x, 0.f) : 0.f;
-                            const float P = valid ? fexp2(fmaf(S[0][j], p.sc2, fmaf(betal, xm, -lse4[e]))) : 0.f;
-                            const float dS = P * (dP[0][j] - del4[e]);
+                            const float P = valid ? fexp2(fmaf(S[j], p.sc2, fmaf(betal, xm, -lse4[e]))) : 0.f;
+                            const float dS = P * (dP[j] - del4[e]);
                             const float gg = (strict && x <= 0.f) ? dS : 0.f;
                             gsum += gg;
                             dbacc = fmaf(dS, xm, dbacc);  // x is +inf where the range is empty
                             g4[e] = gg;
-                            S[0][j] = P;
-                            dP[0][j] = dS;
+                            S[j] = P;
+                            dP[j] = dS;
                         }
                         if (s_valid) *reinterpret_cast<f32x4 *>(p.gd + ((brow + jb) * G + sr) * G + t4) = g4;
                     }
@@ -262,19 +254,19 @@ fpa_bwd_kv_kernel(BwdParams p) {
                 // dV^T[d][s] += dO^T[d][t] P[t][s];  dK^T[d][s] += Q^T[d][t] dS[t][s]
 #pragma unroll
                 for (int dt = 0; dt < NDT; ++dt) {
-                    dvacc[dt] = mma_p2_p3<T, 1, true>(dvacc[dt], S, Dt + 32 * mt * PQ, PQ, 32 * dt, lane);
-                    dkacc[dt] = mma_p2_p3<T, 1, true>(dkacc[dt], dP, Qt + 32 * mt * PQ, PQ, 32 * dt, lane);
+                    dvacc[dt] = mma_p2_p3_pad<T, DT, true>(dvacc[dt], S, Dt, 32 * mt, 32 * dt, lane);
+                    dkacc[dt] = mma_p2_p3_pad<T, DT, true>(dkacc[dt], dP, Qt, 32 * mt, 32 * dt, lane);
                 }
             }
             if (ib > jb) {  // close query block ib: key-block and middle-block soft-min sums
                 if (rs > ninf()) Wacc = fmaf(fexp2(Cs - rs), wblk, Wacc);
                 if (ib > jb + 1) {
                     const float tp = wave_sum((rs > ninf()) ? fexp2(cmid - rs) * wblk : 0.f);
-                    if (lane == 0) p.tbuf[((brow + ib) * p.NB + jb) * 2 + (w & 1)] = tp;
+                    if (lane == 0) p.tbuf[((brow + ib) * p.NB + jb) * 2 + ((kw0 / 32) & 1)] = tp;
                 }
             }
         }
-        if (ib + 1 < p.NB) lstore(buf ^ 1);
+        wait_loads();
         __syncthreads();
     }
 
@@ -282,8 +274,8 @@ fpa_bwd_kv_kernel(BwdParams p) {
     gsum = sum_halves(gsum);
     Wacc = sum_halves(Wacc);
     const float dbw = wave_sum(dbacc);
-    if (lane == 0) p.dbp[((int64_t)bh * p.NKV + kt) * 4 + w] = dbw;  // 0 for waves past T
     if (!wave_active) return;
+    if (lane == 0) p.dbp[(int64_t)bh * p.NK32 + kw0 / 32] = dbw;  // one partial per 32-key group
     if (g == 0 && s < p.TP) p.wsum[rowbase + s] = Wacc;
     if (g == 0 && s_valid) p.dpsi[(int64_t)bh * p.T + s] = -beta * gsum;
     if (!s_valid) return;
@@ -322,8 +314,9 @@ static hipError_t launch_prep_t(const BwdParams &p, hipStream_t s) {
 
 template <typename T, int D>
 static hipError_t launch_kv_t(const BwdParams &p, hipStream_t s) {
-    constexpr int WPE = (D >= 128 || (sizeof(T) == 4 && D >= 64)) ? 1 : FPA_KV_WPE;
-    hipLaunchKernelGGL((fpa_bwd_kv_kernel<T, D, WPE>), dim3(p.NKV, p.BH), dim3(NTHREADS), 0, s, p);
+    constexpr int NW = FPA_NW, WPE = (D >= 128 || (sizeof(T) == 4 && D >= 64)) ? 1 : FPA_KV_WPE;
+    const int nkt = (p.T + 32 * NW - 1) / (32 * NW);
+    hipLaunchKernelGGL((fpa_bwd_kv_kernel<T, D, WPE, NW>), dim3(nkt, p.BH), dim3(64 * NW), 0, s, p);
     return hipGetLastError();
 }
 

@@ -1,9 +1,10 @@
 // fpa_bwd_q.hip -- query-side backward of First Passage Attention.
 //
 // Reference behaviour: _bwd_q (kernel.py:286-340) of yliu-fort/first-passage-attention.
-// gfx950 design: a workgroup of 4 waves owns 128 queries (one query per lane column)
-// and streams 64-key blocks from the diagonal down to key 0 through double-buffered
-// LDS (register prefetch of the next block, one barrier per block).  Each wave
+// gfx950 design: a workgroup of FPA_NW waves owns 32 queries per wave (one query per lane
+// column) and streams 64-key blocks from the diagonal down to key 0 through
+// double-buffered, padded LDS tiles filled by direct global->LDS loads (one barrier per
+// block).  Each wave
 // recomputes S^T = K Q^T and dP^T = V dO^T with Q, dO in registers, accumulates
 // dQ^T += K^T dS^T on the 32x32 MFMA (K^T read from the row-major tile with LDS
 // transpose reads), and reduces per query the query-block soft-min sum
@@ -25,18 +26,18 @@
 
 namespace fpa {
 
-template <typename T, int D, int WPE>
-__global__ void __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+template <typename T, int D, int WPE, int NW>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 fpa_bwd_q_kernel(BwdParams p) {
-    constexpr int BM = 128, BK = 64;  // queries per workgroup, keys per iteration (one block)
+    constexpr int BM = 32 * NW, BK = 64;  // queries per workgroup, keys per iteration (one block)
     constexpr int DT = D < 32 ? 32 : D;
     constexpr int NDT = DT / 32;
-    constexpr int PK = D + (sizeof(T) == 2 ? 8 : 4);
-    constexpr int TS = BK * PK;
-    __shared__ __attribute__((aligned(16))) T Ks[2 * TS + (DT - D)];
-    __shared__ __attribute__((aligned(16))) T Vs[2 * TS];
-    __shared__ __attribute__((aligned(16))) float kSP[2][BK], kPSI[2][BK], kSUFL[2][BK], kPHI[2][BK];
-    __shared__ __attribute__((aligned(16))) float Aw[4][BK];  // per-wave key factors of the shared-reference path
+    constexpr int TB = Pad<T, DT>::template bytes<BK>();  // one padded K or V tile
+    __shared__ __attribute__((aligned(1024))) char Ks[2][TB];
+    __shared__ __attribute__((aligned(1024))) char Vs[2][TB];
+    // Per-key values of a block: SUF, PSI, SUFL, PHI.
+    __shared__ __attribute__((aligned(1024))) float kst[2][4][BK];
+    __shared__ __attribute__((aligned(16))) float Aw[NW][BK];  // per-wave key factors of the shared-reference path
 
     const int tid = threadIdx.x, lane = tid % 64, g = lane / 32, c = lane % 32;
     const int w = __builtin_amdgcn_readfirstlane(tid / 64);  // wave index, uniform across the wave
@@ -56,13 +57,28 @@ fpa_bwd_q_kernel(BwdParams p) {
     const T *Kb = static_cast<const T *>(p.k) + b * p.sk.b + h * p.sk.h;
     const T *Vb = static_cast<const T *>(p.v) + b * p.sv.b + h * p.sv.h;
     const T *DOb = static_cast<const T *>(p.dout) + b * p.sdo.b + h * p.sdo.h;
+    // lanes 0-15: SUF, 16-31: PSI, 32-47: SUFL, 48-63: PHI
+    const int kpl = (lane < 16) ? PL_SUF : (lane < 32) ? PL_PSI : (lane < 48) ? PL_SUFL : PL_PHI;
+    const float *kst_src = p.state + L.plane(kpl) + rowbase + 4 * (lane & 15);
+
+    TileLoader<T, D, DT, BK, NW> kld, vld;
+    kld.init(p.sk.t, w, lane);
+    vld.init(p.sv.t, w, lane);
+    auto issue = [&](int jb, int buf) {
+        kld.issue(Ks[buf], Kb, p.sk.t, jb * BK, p.T, w, lane);
+        vld.issue(Vs[buf], Vb, p.sv.t, jb * BK, p.T, w, lane);
+        if (w == NW - 1) gl_lds16(kst_src + jb * BK, &kst[buf][0][0]);
+    };
+    const int jbmax = min(p.NB - 1, (q0 + BM - 1) / BK);
+    issue(jbmax, 0);
 
     OpRow<T, D> qreg, doreg;
     load_row_p1<T, D>(qreg, Qb + (int64_t)tq * p.sq.t, t_valid, g);
     load_row_p1<T, D>(doreg, DOb + (int64_t)tq * p.sdo.t, t_valid, g);
 
     const float betal = p.beta[h] * LOG2E;
-    float lse = 0.f, del = 0.f, pre = 0.f, prel = 0.f;
+    // Rows past T: lse = +inf makes P = 0 with no per-element mask.
+    float lse = pinf(), del = 0.f, pre = 0.f, prel = 0.f;
     if (t_valid) {
         lse = p.lse[rowbase + tq];
         del = p.delta[rowbase + tq];
@@ -71,10 +87,6 @@ fpa_bwd_q_kernel(BwdParams p) {
     }
     const float ct = -pre * p.il2;  // max a over [start of blk(t), t]
     const float prel_ct = fexp2(prel - ct);
-
-    if constexpr (D < DT) {
-        for (int i = tid; i < 2 * TS + (DT - D); i += NTHREADS) Ks[i] = (T)0.f;
-    }
 
     f32x16 dqacc[NDT];
 #pragma unroll
@@ -85,39 +97,14 @@ fpa_bwd_q_kernel(BwdParams p) {
     const float a_first = -p.state[L.plane(PL_PHI) + rowbase + ibc * G] * p.il2;  // a of the block's first query
     const float c_blk = -p.state[L.bplane(BP_MIN) + brow + ibc] * p.il2;          // max a over block ib
 
-    TileRegs<T, D, BK> kr, vr;
-    float pf_suf = 0.f, pf_psi = 0.f, pf_sufl = 0.f, pf_phi = 0.f;
-    auto gload = [&](int jb) {
-        kr.load(Kb, p.sk.t, jb * BK, p.T);
-        vr.load(Vb, p.sv.t, jb * BK, p.T);
-        if (tid < BK) {
-            const int64_t r = rowbase + jb * BK + tid;
-            pf_suf = p.state[L.plane(PL_SUF) + r];
-            pf_psi = p.state[L.plane(PL_PSI) + r];
-            pf_sufl = p.state[L.plane(PL_SUFL) + r];
-            pf_phi = p.state[L.plane(PL_PHI) + r];
-        }
-    };
-    auto lstore = [&](int buf) {
-        kr.store(Ks + buf * TS, PK);
-        vr.store(Vs + buf * TS, PK);
-        if (tid < BK) {
-            kSP[buf][tid] = pf_suf - pf_psi;
-            kPSI[buf][tid] = pf_psi;
-            kSUFL[buf][tid] = pf_sufl;
-            kPHI[buf][tid] = pf_phi;
-        }
-    };
-
-    const int jbmax = min(p.NB - 1, (q0 + BM - 1) / BK);
-    gload(jbmax);
-    lstore(0);
+    wait_loads();
     __syncthreads();
     for (int jb = jbmax, it = 0; jb >= 0; --jb, ++it) {
         const int buf = it & 1;
         const int s0 = jb * BK;
-        if (jb > 0) gload(jb - 1);
+        if (jb > 0) issue(jb - 1, buf ^ 1);
         if (wave_active && jb <= ib) {
+            const float *kSUF = kst[buf][0], *kPSI = kst[buf][1], *kSUFL = kst[buf][2], *kPHI = kst[buf][3];
             if (jb + 1 < ib) {  // block jb + 1 joins the middle
                 const float bm = p.state[L.bplane(BP_MIN) + brow + jb + 1];
                 mid = fminf(mid, bm);
@@ -133,51 +120,47 @@ fpa_bwd_q_kernel(BwdParams p) {
                 R = fmaxf(fmaxf(cfirst, cmid), c_blk);
                 fast = FPA_Q_FAST && (R - fmaxf(cmid, a_first)) < FAST_SPREAD;
                 if (fast) {
-                    Aw[w][lane] = fexp2(kSUFL[buf][lane] - R) + fexp2(midl - R);
+                    Aw[w][lane] = fexp2(kSUFL[lane] - R) + fexp2(midl - R);
                     bq = t_valid ? fexp2(prel - R) : 1.f;  // rows past T: any positive factor (g = 0)
                 }
             }
             float rblk = 0.f;  // sum of g / (Z 2^{-R}) over this key block (shared-reference path)
             const float Y = fminf(pre, mid);
             const bool diag = (jb == ib);
-            const bool full = qw0 + 32 <= p.T;
             const int tr = tq - s0;
-            const T *Kt = Ks + buf * TS;
-            const T *Vt = Vs + buf * TS;
+            const char *Kt = Ks[buf];
+            const char *Vt = Vs[buf];
             float r = pinf();  // running min of phi over [u, t] for the in-block scan
 #pragma unroll 1
             for (int mt = 1; mt >= 0; --mt) {
-                f32x16 S[1], dP[1];
-                S[0] = mma_p1_lds_reg<T, D>(zero16(), Kt + (32 * mt + c) * PK, g, qreg);   // [s][t]
-                dP[0] = mma_p1_lds_reg<T, D>(zero16(), Vt + (32 * mt + c) * PK, g, doreg);
+                f32x16 S = mma_p1_pad_reg<T, D, DT>(zero16(), Kt, 32 * mt + c, g, qreg);   // [s][t]
+                f32x16 dP = mma_p1_pad_reg<T, D, DT>(zero16(), Vt, 32 * mt + c, g, doreg);
                 float X[16];
-                if (diag) diag_x_keys(X, r, kPHI[buf], mt, tr, g);  // X_ts = min phi(s, t] in the block
+                if (diag) diag_x_keys(X, r, kPHI, mt, tr, g);  // X_ts = min phi(s, t] in the block
                 if (!diag) {
-                    // Off the diagonal block every key is valid and earlier than every query;
-                    // only query rows past T (ragged last block) are masked.
+                    // Off the diagonal block every key is valid and earlier than every query.
                     auto offdiag = [&](auto fast_c) {
                         constexpr bool FAST = decltype(fast_c)::value;
 #pragma unroll
                         for (int jq = 0; jq < 4; ++jq) {
                             const int s4 = 32 * mt + 8 * jq + 4 * g;
-                            const f32x4 sp4 = *reinterpret_cast<const f32x4 *>(&kSP[buf][s4]);
-                            const f32x4 psi4 = *reinterpret_cast<const f32x4 *>(&kPSI[buf][s4]);
+                            const f32x4 suf4 = *reinterpret_cast<const f32x4 *>(&kSUF[s4]);
+                            const f32x4 psi4 = *reinterpret_cast<const f32x4 *>(&kPSI[s4]);
                             const f32x4 zk4 = FAST ? *reinterpret_cast<const f32x4 *>(&Aw[w][s4])
-                                                   : *reinterpret_cast<const f32x4 *>(&kSUFL[buf][s4]);
+                                                   : *reinterpret_cast<const f32x4 *>(&kSUFL[s4]);
 #pragma unroll
                             for (int e = 0; e < 4; ++e) {
                                 const int j = 4 * jq + e;
-                                const float x = fminf(sp4[e], Y - psi4[e]);  // min(SUF_s, MID, PRE_t) - psi_s
+                                const float x = fminf(suf4[e], Y) - psi4[e];  // min(SUF_s, MID, PRE_t) - psi_s
                                 const float xm = fminf(x, 0.f);
-                                float P = fexp2(fmaf(S[0][j], p.sc2, fmaf(betal, xm, -lse)));
-                                if (!full) P = t_valid ? P : 0.f;
-                                const float dS = P * (dP[0][j] - del);
+                                const float P = fexp2(fmaf(S[j], p.sc2, fmaf(betal, xm, -lse)));
+                                const float dS = P * (dP[j] - del);
                                 const float gg = (x <= 0.f) ? dS : 0.f;
                                 if constexpr (FAST)
                                     rblk = fmaf(gg, frcp(zk4[e] + bq), rblk);
                                 else
                                     racc = fmaf(gg, frcp(fexp2(zk4[e] - ct) + mterm), racc);
-                                S[0][j] = dS;
+                                S[j] = dS;
                             }
                         }
                     };
@@ -191,7 +174,7 @@ fpa_bwd_q_kernel(BwdParams p) {
 #pragma unroll
                     for (int jq = 0; jq < 4; ++jq) {
                         const int s4 = 32 * mt + 8 * jq + 4 * g;
-                        const f32x4 psi4 = *reinterpret_cast<const f32x4 *>(&kPSI[buf][s4]);
+                        const f32x4 psi4 = *reinterpret_cast<const f32x4 *>(&kPSI[s4]);
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const int j = 4 * jq + e;
@@ -199,19 +182,19 @@ fpa_bwd_q_kernel(BwdParams p) {
                             const bool valid = t_valid && (s <= tq);
                             const bool strict = valid && (s < tq);
                             const float xm = strict ? fminf(X[j] - psi4[e], 0.f) : 0.f;
-                            const float P = valid ? fexp2(fmaf(S[0][j], p.sc2, fmaf(betal, xm, -lse))) : 0.f;
-                            S[0][j] = P * (dP[0][j] - del);
+                            const float P = valid ? fexp2(fmaf(S[j], p.sc2, fmaf(betal, xm, -lse))) : 0.f;
+                            S[j] = P * (dP[j] - del);
                         }
                     }
                 }
                 // dQ^T[d][t] += K^T[d][s] dS^T[s][t]   (K read transposed from its natural layout)
 #pragma unroll
                 for (int dt = 0; dt < NDT; ++dt)
-                    dqacc[dt] = mma_p2_p3<T, 1, true>(dqacc[dt], S, Kt + 32 * mt * PK, PK, 32 * dt, lane);
+                    dqacc[dt] = mma_p2_p3_pad<T, DT, true>(dqacc[dt], S, Kt, 32 * mt, 32 * dt, lane);
             }
             if (fast) racc = fmaf(fexp2(ct - R), rblk, racc);  // R_t gets 2^{c_t} sum g / Z
         }
-        if (jb > 0) lstore(buf ^ 1);
+        wait_loads();
         __syncthreads();
     }
 
@@ -241,9 +224,10 @@ fpa_bwd_q_kernel(BwdParams p) {
 
 template <typename T, int D>
 static hipError_t launch_q_t(const BwdParams &p, hipStream_t s) {
-    const int nqt = (p.T + 127) / 128;
+    constexpr int NW = FPA_NW;
+    const int nqt = (p.T + 32 * NW - 1) / (32 * NW);
     constexpr int WPE = (D >= 128) ? 1 : FPA_Q_WPE;
-    hipLaunchKernelGGL((fpa_bwd_q_kernel<T, D, WPE>), dim3(nqt, p.BH), dim3(NTHREADS), 0, s, p);
+    hipLaunchKernelGGL((fpa_bwd_q_kernel<T, D, WPE, NW>), dim3(nqt, p.BH), dim3(64 * NW), 0, s, p);
     return hipGetLastError();
 }
 

@@ -40,6 +40,12 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr int G = 64;        // statistics block
 constexpr int NTHREADS = 256;
+// Waves per workgroup of the three main kernels: each wave owns 32 queries (forward, query side)
+// or 32 keys (key side), so a workgroup covers 32 * FPA_NW rows and its LDS tiles are shared by
+// FPA_NW waves.
+#ifndef FPA_NW
+#define FPA_NW 4
+#endif
 
 __device__ __forceinline__ float pinf() { return __builtin_inff(); }
 __device__ __forceinline__ float ninf() { return -__builtin_inff(); }
@@ -65,6 +71,7 @@ __device__ __forceinline__ float uniform_f(float x) {  // value of the first act
 // A tile of soft-min terms whose exponents span less than this many binades uses one shared
 // reference (products of per-key and per-query factors); wider tiles use per-element references.
 constexpr float FAST_SPREAD = 96.f;
+constexpr float PROD_SPREAD = 100.f;  // max PREL spread of a query block for the product form of Z
 
 __device__ __forceinline__ f32x16 zero16() {
     f32x16 z;
@@ -305,27 +312,27 @@ __device__ __forceinline__ float max_halves(float x) {
 }
 
 // ---------------------------------------------------------------------------
-// Swizzled LDS tiles filled by direct global -> LDS loads.
+// LDS tiles filled by direct global -> LDS loads.
 //
-// A tile of NR rows x D elements is stored unpadded (D * sizeof(T) bytes per row) in
-// 16-byte chunks; logical chunk lc of row r sits at physical chunk lc ^ (r & SW), which
-// spreads a column of chunks over the LDS banks.  global_load_lds_dwordx4 writes the 16
-// bytes of lane l of a wave to (LDS base + 16 * l): each wave instruction fills 64
-// consecutive slots, and each lane picks the global row/chunk that belongs in its slot.
-// Rows at or past T are loaded from row T - 1 (finite values that callers mask).
+// A tile holds NR rows of DT elements (DT = D rounded up to 32) at a pitch of DT + one
+// 16-byte chunk: row r starts at byte r * ROWB, so every LDS read of a lane is a per-lane
+// base plus an immediate offset, and a 16-lane group reading one chunk column touches 16
+// distinct bank groups (ROWB / 16 is odd).  global_load_lds_dwordx4 writes the 16 bytes of
+// lane l of a wave to (LDS base + 16 * l): each wave instruction fills 64 consecutive
+// chunk slots of the tile, and each lane fetches the global chunk that belongs in its
+// slot.  Pad slots and the chunks of columns D..DT-1 fetch a real chunk of the same row
+// (finite values whose products are discarded), and rows at or past T fetch row T - 1
+// (finite values that the callers mask).
 // ---------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void gbl_void_t;
 
-template <typename T, int D> struct Sw {
-    static constexpr int CE = 16 / sizeof(T);           // elements per chunk
-    static constexpr int CPR = D / CE;                   // chunks per row
-    static constexpr int SW = (CPR < 8 ? CPR : 8) - 1;   // swizzle mask
-    static constexpr int ROWB = D * sizeof(T);           // bytes per row
-    // byte offset of element e (a multiple of 4 elements for fp16) of row r
-    __device__ static __forceinline__ int off(int r, int e) {
-        return r * ROWB + (((e / CE) ^ (r & SW)) << 4) + (e % CE) * (int)sizeof(T);
-    }
+template <typename T, int DT> struct Pad {
+    static constexpr int CE = 16 / sizeof(T);  // elements per chunk
+    static constexpr int CPR = DT / CE;        // chunks of a row
+    static constexpr int CPRP = CPR + 1;       // with the pad chunk
+    static constexpr int PITCH = DT + CE;      // elements
+    static constexpr int ROWB = PITCH * sizeof(T);
     template <int NR> static constexpr int bytes() { return NR * ROWB; }
 };
 
@@ -333,94 +340,91 @@ __device__ __forceinline__ void gl_lds16(const void *src, void *lds_dst) {
     __builtin_amdgcn_global_load_lds((gbl_void_t *)(src), (lds_void_t *)(lds_dst), 16, 0, 0);
 }
 
-// Issue the loads of rows [row0, row0 + NR) of a (B, H, T, D)-strided tensor into the swizzled
-// tile at `tile` (all waves of the workgroup take part; completes at the next vmcnt(0) wait).
-template <typename T, int D, int NR>
-__device__ __forceinline__ void tile_issue(char *tile, const T *base, int64_t st, int row0, int T_, int wave, int lane) {
-    using S = Sw<T, D>;
-    constexpr int NI = NR * S::CPR / 64;  // wave instructions per tile
-    static_assert(NR * S::CPR % 64 == 0, "tile must fill whole wave instructions");
-    for (int i = wave; i < NI; i += NTHREADS / 64) {
-        const int k = 64 * i + lane;
-        const int r = k / S::CPR, pc = k % S::CPR, lc = pc ^ (r & S::SW);
-        const int row = min(row0 + r, T_ - 1);
-        gl_lds16(base + (int64_t)row * st + lc * S::CE, tile + 1024 * i);
-    }
-}
-
-// Load n consecutive floats (n <= 256, multiple of 4) from global into LDS with one wave.
-__device__ __forceinline__ void vec_issue(float *lds, const float *src, int n, int lane) {
-    if (4 * lane < n) gl_lds16(src + 4 * lane, lds);
-}
-
 __device__ __forceinline__ void wait_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// P1 operands from a swizzled tile row.
-template <typename T, int K>
-__device__ __forceinline__ f32x16 mma_p1_sw_reg(f32x16 acc, const char *tile, int row, int g, const OpRow<T, K> &breg) {
-    using S = Sw<T, K>;
-    if constexpr (sizeof(T) == 2) {
+// Loads NR-row tiles of one (B, H, T, D)-strided tensor (d stride 1, rows 16-byte aligned,
+// 64 * row stride < 2^31 bytes) into padded LDS tiles.  The NI wave instructions of a tile
+// are shared out over the NW waves of the workgroup; each wave keeps the byte offsets of its
+// lanes' source chunks relative to the tile's first row, so a full tile costs no VALU work.
+template <typename T, int D, int DT, int NR, int NW> struct TileLoader {
+    using P = Pad<T, DT>;
+    static constexpr int CPRD = D / P::CE;                // chunks of data in a row
+    static constexpr int NI = NR * P::CPRP / 64;          // wave instructions per tile
+    static constexpr int PER = (NI + NW - 1) / NW;        // per wave
+    static_assert(NR * P::CPRP % 64 == 0, "a tile fills whole wave instructions");
+    uint32_t off[PER];
+    __device__ static __forceinline__ void slot(int i, int lane, int &r, int &lc) {
+        const int k = 64 * i + lane;
+        r = k / P::CPRP;
+        const int pc = k % P::CPRP;
+        lc = (pc < CPRD) ? pc : pc % CPRD;
+    }
+    __device__ __forceinline__ void init(int64_t st, int wave, int lane) {
 #pragma unroll
-        for (int i = 0; i < K / 16; ++i)
-            acc = MT<T>::mma(*reinterpret_cast<const h8 *>(tile + S::off(row, 16 * i + 8 * g)), breg[i], acc);
-    } else {
-#pragma unroll
-        for (int i = 0; i < K / 8; ++i) {
-            const f32x4 a = *reinterpret_cast<const f32x4 *>(tile + S::off(row, g * (K / 2) + 4 * i));
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc = MT<T>::mma(a[e], breg[4 * i + e], acc);
+        for (int j = 0; j < PER; ++j) {
+            int r, lc;
+            slot(wave + NW * j, lane, r, lc);
+            off[j] = (uint32_t)((r * st + lc * P::CE) * (int64_t)sizeof(T));
         }
     }
-    return acc;
+    // Rows row0 .. row0 + NR - 1 of the tensor whose row 0 is `base` into `tile`.
+    __device__ __forceinline__ void issue(char *tile, const T *base, int64_t st, int row0, int T_, int wave,
+                                          int lane) const {
+        const char *b0 = reinterpret_cast<const char *>(base + (int64_t)row0 * st);
+        if (row0 + NR <= T_) {
+#pragma unroll
+            for (int j = 0; j < PER; ++j) {
+                const int i = wave + NW * j;
+                if (NI % NW == 0 || i < NI) gl_lds16(b0 + off[j], tile + 1024 * i);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < PER; ++j) {
+                const int i = wave + NW * j;
+                if (NI % NW == 0 || i < NI) {
+                    int r, lc;
+                    slot(i, lane, r, lc);
+                    const int row = min(row0 + r, T_ - 1);
+                    gl_lds16(base + (int64_t)row * st + lc * P::CE, tile + 1024 * i);
+                }
+            }
+        }
+    }
+};
+
+// acc += A * B over a contraction of length K: A = P1 operands of row `row` of a padded tile
+// of width DT, B = P1 operands in registers.
+template <typename T, int K, int DT>
+__device__ __forceinline__ f32x16 mma_p1_pad_reg(f32x16 acc, const char *tile, int row, int g, const OpRow<T, K> &breg) {
+    return mma_p1_lds_reg<T, K>(acc, reinterpret_cast<const T *>(tile) + row * Pad<T, DT>::PITCH, g, breg);
 }
 
-// acc += A * B with the P3 operand from a swizzled tile (rows = contraction, column n = ncol0 + c)
-// and the P2 operand from the accumulator tile c0 (rows 32*mt0 .. of the tile are its rows).
-template <typename T, int D, bool A_IS_P3>
-__device__ __forceinline__ f32x16 mma_p2_p3_sw(f32x16 acc, const f32x16 &c0, const char *tile, int row0, int ncol0,
-                                               int lane) {
-    using S = Sw<T, D>;
-    const int g = lane >> 5;
-    if constexpr (sizeof(T) == 2) {
-        const int j = lane & 15, q = lane >> 4;
-        const int col = ncol0 + 16 * (q & 1) + 4 * (j & 3);
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-            h8 p2;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) p2[e] = (f16)c0[8 * hf + e];
-            const int row = row0 + 16 * hf + 4 * (q >> 1) + (j >> 2);
-            const h4 lo = ds_read_tr16(reinterpret_cast<const f16 *>(tile + S::off(row, col)));
-            const h4 hi = ds_read_tr16(reinterpret_cast<const f16 *>(tile + S::off(row + 8, col)));
-            const h8 p3 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            acc = A_IS_P3 ? MT<T>::mma(p3, p2, acc) : MT<T>::mma(p2, p3, acc);
-        }
-    } else {
-        const int n = ncol0 + (lane & 31);
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const float p3 = *reinterpret_cast<const float *>(tile + S::off(row0 + acc_row(j, g), n));
-            acc = A_IS_P3 ? MT<T>::mma(p3, c0[j], acc) : MT<T>::mma(c0[j], p3, acc);
-        }
-    }
-    return acc;
+// acc += A * B with the P3 operand from a padded tile (contraction over its rows row0 .. row0 + 31,
+// column n = ncol0 + lane % 32) and the P2 operand from the accumulator tile c0 (its rows are the
+// contraction index).  A_IS_P3: the P3 value is A.
+template <typename T, int DT, bool A_IS_P3>
+__device__ __forceinline__ f32x16 mma_p2_p3_pad(f32x16 acc, const f32x16 &c0, const char *tile, int row0, int ncol0,
+                                                int lane) {
+    const f32x16 c[1] = {c0};
+    return mma_p2_p3<T, 1, A_IS_P3>(acc, c, reinterpret_cast<const T *>(tile) + row0 * Pad<T, DT>::PITCH,
+                                    Pad<T, DT>::PITCH, ncol0, lane);
 }
 
 // ---------------------------------------------------------------------------
 // Register prefetch of an NR x D tile of a (B, H, T, D)-strided tensor (rows row0 + r,
 // zero past T), stored afterwards into a natural-layout LDS tile of the given pitch.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int NR> struct TileRegs {
+template <typename T, int D, int NR, int NTH> struct TileRegs {
     static constexpr int CE = MT<T>::CHUNK;
     static constexpr int CPR = D / CE;
     static constexpr int NCH = NR * CPR;
-    static constexpr int PER = (NCH + NTHREADS - 1) / NTHREADS;
+    static constexpr int PER = (NCH + NTH - 1) / NTH;
     f32x4 r[PER];
     __device__ __forceinline__ void load(const T *base, int64_t st, int row0, int T_) {
-        if (row0 + NR <= T_ && NCH % NTHREADS == 0) {  // full tile: no per-row guard
+        if (row0 + NR <= T_ && NCH % NTH == 0) {  // full tile: no per-row guard
 #pragma unroll
             for (int i = 0; i < PER; ++i) {
-                const int idx = threadIdx.x + i * NTHREADS;
+                const int idx = threadIdx.x + i * NTH;
                 const int row = idx / CPR, cc = idx % CPR;
                 r[i] = *reinterpret_cast<const f32x4 *>(base + (int64_t)(row0 + row) * st + cc * CE);
             }
@@ -428,7 +432,7 @@ template <typename T, int D, int NR> struct TileRegs {
         }
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            const int idx = threadIdx.x + i * NTHREADS;
+            const int idx = threadIdx.x + i * NTH;
             const int row = idx / CPR, cc = idx % CPR;
             f32x4 v = {0.f, 0.f, 0.f, 0.f};
             if (idx < NCH && row0 + row < T_)
@@ -439,7 +443,7 @@ template <typename T, int D, int NR> struct TileRegs {
     __device__ __forceinline__ void store(T *dst, int pitch) const {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            const int idx = threadIdx.x + i * NTHREADS;
+            const int idx = threadIdx.x + i * NTH;
             const int row = idx / CPR, cc = idx % CPR;
             if (idx < NCH) *reinterpret_cast<f32x4 *>(dst + row * pitch + cc * CE) = r[i];
         }

@@ -4,9 +4,9 @@
 // yliu-fort/first-passage-attention.  Same maths, gfx950 design:
 //   * statistics: one wave per block of G = 64 positions, prefix/suffix min and
 //     base-2 log-sum-exp by wave shuffles;
-//   * forward: a workgroup of 4 waves owns 128 query rows (32 per wave), streams
-//     64-key tiles from the diagonal down to key 0 through double-buffered LDS
-//     (register prefetch of the next tile, one barrier per tile), computes
+//   * forward: a workgroup of FPA_NW waves owns 32 query rows per wave, streams
+//     64-key tiles from the diagonal down to key 0 through double-buffered, padded
+//     LDS tiles filled by direct global->LDS loads (one barrier per tile), computes
 //     S^T = K Q^T and O^T += V^T P^T on the 32x32 MFMA (V^T read from the row-major
 //     tile with LDS transpose reads), and keeps each query's online-softmax state in
 //     its own lane.
@@ -102,17 +102,17 @@ hipError_t launch_stats(const StatsParams &p, hipStream_t s) {
 // ---------------------------------------------------------------------------
 constexpr float RESCALE_SLACK = 8.f;
 
-template <typename T, int D, int WPE>
-__global__ void __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+template <typename T, int D, int WPE, int NW>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 fpa_fwd_kernel(FwdParams p) {
-    constexpr int BM = 128, BN = 64;
+    constexpr int BM = 32 * NW, BN = 64;
     constexpr int DT = D < 32 ? 32 : D;
     constexpr int NDT = DT / 32;
-    constexpr int PK = D + (sizeof(T) == 2 ? 8 : 4);  // tile pitch (elements)
-    constexpr int TS = BN * PK;                          // one tile
-    __shared__ __attribute__((aligned(16))) T Ks[2 * TS];
-    __shared__ __attribute__((aligned(16))) T Vs[2 * TS + (DT - D)];
-    __shared__ __attribute__((aligned(16))) float cA[2][BN], cP[2][BN], cPHI[2][BN];
+    constexpr int TB = Pad<T, DT>::template bytes<BN>();  // one padded K or V tile
+    __shared__ __attribute__((aligned(1024))) char Ks[2][TB];
+    __shared__ __attribute__((aligned(1024))) char Vs[2][TB];
+    // Per-key values of a tile: CA, CP, PHI (and a copy of PHI that fills the load instruction).
+    __shared__ __attribute__((aligned(1024))) float cst[2][4][BN];
 
     const int tid = threadIdx.x, lane = tid % 64, g = lane / 32, c = lane % 32;
     const int w = __builtin_amdgcn_readfirstlane(tid / 64);  // wave index, uniform across the wave
@@ -129,6 +129,23 @@ fpa_fwd_kernel(FwdParams p) {
     const T *Qb = static_cast<const T *>(p.q) + b * p.sq.b + h * p.sq.h;
     const T *Kb = static_cast<const T *>(p.k) + b * p.sk.b + h * p.sk.h;
     const T *Vb = static_cast<const T *>(p.v) + b * p.sv.b + h * p.sv.h;
+    // lanes 0-15: CA, 16-31: CP, 32-63: PHI (the state planes hold TP >= every tile end rows)
+    const float *cst_src = p.state + ((lane < 16) ? L.plane(PL_CA) : (lane < 32) ? L.plane(PL_CP) : L.plane(PL_PHI)) +
+                           rowbase + 4 * (lane & 15);
+
+    // Tile jt of K, V and the per-key values into buffer `buf` (shared out over the waves).
+    TileLoader<T, D, DT, BN, NW> kld, vld;
+    kld.init(p.sk.t, w, lane);
+    vld.init(p.sv.t, w, lane);
+    auto issue = [&](int jt, int buf) {
+        kld.issue(Ks[buf], Kb, p.sk.t, jt * BN, p.T, w, lane);
+        vld.issue(Vs[buf], Vb, p.sv.t, jt * BN, p.T, w, lane);
+        if (w == NW - 1) gl_lds16(cst_src + jt * BN, &cst[buf][0][0]);
+    };
+
+    const int nkt = (p.T + BN - 1) / BN;
+    const int jtmax = min(nkt - 1, (q0 + BM - 1) / BN);
+    issue(jtmax, 0);
 
     OpRow<T, D> qreg;
     load_row_p1<T, D>(qreg, Qb + (int64_t)tq * p.sq.t, tq < p.T, g);
@@ -141,49 +158,20 @@ fpa_fwd_kernel(FwdParams p) {
     f32x16 oacc[NDT];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) oacc[dt] = zero16();
-
-    const int nkt = (p.T + BN - 1) / BN;
-    const int jtmax = min(nkt - 1, (q0 + BM - 1) / BN);
     float mid = pinf();  // min phi over the blocks strictly between the key block and ib
 
-    TileRegs<T, D, BN> kr, vr;
-    float pf_suf = 0.f, pf_psi = 0.f, pf_phi = 0.f;
-    auto gload = [&](int jt) {
-        kr.load(Kb, p.sk.t, jt * BN, p.T);
-        vr.load(Vb, p.sv.t, jt * BN, p.T);
-        if (tid < BN) {
-            const int64_t r = rowbase + jt * BN + tid;
-            pf_suf = p.state[L.plane(PL_SUF) + r];
-            pf_psi = p.state[L.plane(PL_PSI) + r];
-            pf_phi = p.state[L.plane(PL_PHI) + r];
-        }
-    };
-    auto lstore = [&](int buf) {
-        kr.store(Ks + buf * TS, PK);
-        vr.store(Vs + buf * TS, PK);
-        if (tid < BN) {
-            cA[buf][tid] = betal * fminf(pf_suf - pf_psi, 0.f);
-            cP[buf][tid] = betal * pf_psi;
-            cPHI[buf][tid] = pf_phi;
-        }
-    };
-    if constexpr (D < DT) {  // V columns D..31 read by the padded transpose reads stay zero
-        for (int i = tid; i < 2 * TS + (DT - D); i += NTHREADS) Vs[i] = (T)0.f;
-        __syncthreads();
-    }
-
-    gload(jtmax);
-    lstore(0);
+    wait_loads();
     __syncthreads();
     for (int jt = jtmax, it = 0; jt >= 0; --jt, ++it) {
         const int buf = it & 1;
         const int s0 = jt * BN;
-        if (jt > 0) gload(jt - 1);
+        if (jt > 0) issue(jt - 1, buf ^ 1);
         if (wave_active && s0 <= qw0 + 31) {
-            const T *Kt = Ks + buf * TS;
+            const char *Kt = Ks[buf];
+            const float *cA = cst[buf][0], *cP = cst[buf][1], *cPHI = cst[buf][2];
             f32x16 s[2];
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt) s[mt] = mma_p1_lds_reg<T, D>(zero16(), Kt + (32 * mt + c) * PK, g, qreg);
+            for (int mt = 0; mt < 2; ++mt) s[mt] = mma_p1_pad_reg<T, D, DT>(zero16(), Kt, 32 * mt + c, g, qreg);
 
             const int jb = jt;  // BN == G: the key tile is one statistics block
             if (jb < ib) {
@@ -193,8 +181,8 @@ fpa_fwd_kernel(FwdParams p) {
 #pragma unroll
                     for (int jq = 0; jq < 4; ++jq) {
                         const int s4 = 32 * mt + 8 * jq + 4 * g;
-                        const f32x4 a4 = *reinterpret_cast<const f32x4 *>(&cA[buf][s4]);
-                        const f32x4 p4 = *reinterpret_cast<const f32x4 *>(&cP[buf][s4]);
+                        const f32x4 a4 = *reinterpret_cast<const f32x4 *>(&cA[s4]);
+                        const f32x4 p4 = *reinterpret_cast<const f32x4 *>(&cP[s4]);
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const float b2 = __builtin_amdgcn_fmed3f(a4[e], Y - p4[e], E);
@@ -206,14 +194,14 @@ fpa_fwd_kernel(FwdParams p) {
                 const int tr = tq - s0;
                 float X[2][16];
                 float r = pinf();
-                diag_x_keys(X[1], r, cPHI[buf], 1, tr, g);
-                diag_x_keys(X[0], r, cPHI[buf], 0, tr, g);
+                diag_x_keys(X[1], r, cPHI, 1, tr, g);
+                diag_x_keys(X[0], r, cPHI, 0, tr, g);
 #pragma unroll
                 for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
                     for (int jq = 0; jq < 4; ++jq) {
                         const int s4 = 32 * mt + 8 * jq + 4 * g;
-                        const f32x4 p4 = *reinterpret_cast<const f32x4 *>(&cP[buf][s4]);
+                        const f32x4 p4 = *reinterpret_cast<const f32x4 *>(&cP[s4]);
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const int j = 4 * jq + e, sr = s4 + e;
@@ -254,13 +242,15 @@ fpa_fwd_kernel(FwdParams p) {
             l_i += sum_halves(rs);
 
             // O^T[d][t] += V^T[d][s] P^T[s][t]   (V read transposed from its natural layout)
-            const T *Vt = Vs + buf * TS;
 #pragma unroll
-            for (int dt = 0; dt < NDT; ++dt) oacc[dt] = mma_p2_p3<T, 2, true>(oacc[dt], s, Vt, PK, 32 * dt, lane);
+            for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt)
+                    oacc[dt] = mma_p2_p3_pad<T, DT, true>(oacc[dt], s[mt], Vs[buf], 32 * mt, 32 * dt, lane);
 
             if (jb < ib) mid = fminf(mid, p.state[L.bplane(BP_MIN) + (int64_t)bh * p.NB + jb]);
         }
-        if (jt > 0) lstore(buf ^ 1);
+        wait_loads();
         __syncthreads();
     }
 
@@ -291,9 +281,9 @@ fpa_fwd_kernel(FwdParams p) {
 
 template <typename T, int D>
 static hipError_t launch_fwd_t(const FwdParams &p, hipStream_t s) {
-    const int nqt = (p.T + 127) / 128;
-    constexpr int WPE = (D >= 128) ? 1 : FPA_FWD_WPE;
-    hipLaunchKernelGGL((fpa_fwd_kernel<T, D, WPE>), dim3(nqt, p.BH), dim3(NTHREADS), 0, s, p);
+    constexpr int NW = FPA_NW, WPE = (D >= 128) ? 1 : FPA_FWD_WPE;
+    const int nqt = (p.T + 32 * NW - 1) / (32 * NW);
+    hipLaunchKernelGGL((fpa_fwd_kernel<T, D, WPE, NW>), dim3(nqt, p.BH), dim3(64 * NW), 0, s, p);
     return hipGetLastError();
 }
 

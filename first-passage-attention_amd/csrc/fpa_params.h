@@ -48,17 +48,21 @@ struct BwdParams {
     float *dpsi;   // (B, H, T) contiguous
     float *dbeta;  // (H,)
     // workspace regions
-    float *delta;  // BH * TP
+    float *qinfo;  // QI_N planes of BH * TP: per-query values of the backward (QI_*)
+    float *delta;  // = qinfo + QI_DEL * BH * TP
     float *wsum;   // BH * TP   key-block soft-min sums W_s
     float *rsum;   // BH * TP   query-block soft-min sums R_t
     float *gd;     // BH * NB * G * G   gated dS of in-block pairs, [s][t]
     float *tbuf;   // BH * NB * NB * 2  middle-block sums (two 32-key halves)
-    float *dbp;    // BH * NKV * 4      dbeta partials
-    int B, H, T, TP, NB, BH, NKV;
+    float *dbp;    // BH * NK32         dbeta partials, one per 32-key group
+    int B, H, T, TP, NB, BH, NK32;
     float sc2;     // log2(e) / sqrt(D)
     float smscale; // 1 / sqrt(D)
     float il2;     // log2(e) / tau
 };
+
+// Planes of BwdParams::qinfo.
+enum { QI_LSE = 0, QI_DEL = 1, QI_PRE = 2, QI_ZQ = 3, QI_N = 4 };
 
 // Launchers (defined next to their kernels); return hipSuccess or the launch error.
 hipError_t launch_stats(const StatsParams &p, hipStream_t s);

@@ -17,7 +17,8 @@ from . import _lib
 def _rows_ok(t):
     ce = 8 if t.dtype == torch.float16 else 4
     s = t.stride()
-    return s[3] == 1 and t.data_ptr() % 16 == 0 and all(x % ce == 0 for x in s[:3])
+    return (s[3] == 1 and t.data_ptr() % 16 == 0 and all(x % ce == 0 for x in s[:3])
+            and 0 <= s[2] * 64 * t.element_size() < 2 ** 31)
 
 
 def rows(t):
