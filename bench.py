@@ -13,7 +13,9 @@ JSON line.  ``value`` is fwd+bwd TFLOP/s of the algorithmic flops 14*D*P
 
 Per-kernel times come from HIP events recorded on torch's current stream (the stream
 every kernel is launched on) around C-ABI calls that enqueue one kernel each; the
-dominant kernel's duration gives ``roofline``.  ``cpu_baseline`` times the float32
+dominant kernel's duration gives ``roofline``.  ``roofline.traffic`` is that kernel's HBM
+bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
+(profiles/fpa_<config>_traffic.txt), null when the workload has none.  ``cpu_baseline`` times the float32
 CPU oracle (a port of the reference's dense path) on a bounded sample of heads of
 the same workload.
 """
@@ -54,6 +56,18 @@ def make_inputs(cfg, seed=0):
     else:
         beta = torch.nn.functional.softplus(torch.randn(H, generator=g))
     return q, k, v, phi, psi, beta, do
+
+
+def measured_traffic(config, kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+    (profiles/fpa_<config>_traffic.txt), or None when there is none for this workload."""
+    path = os.path.join(ROOT, "profiles", f"fpa_{config}_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith(kernel + ":"):
+            return int(float(line.split(":", 1)[1]))
+    return None
 
 
 def pairs(cfg):
@@ -210,7 +224,8 @@ def main():
         "fwd_bwd_pct_peak": round(100 * fb_tflops / peak, 2),
         "kernel_ms": {n: round(t, 4) for n, (t, _) in kernels.items()},
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 3), "peak": peak,
-                     "unit": "TFLOP/s", "frac": round(achieved / peak, 4), "traffic": None},
+                     "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
+                     "traffic": measured_traffic(a.config, dom)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)

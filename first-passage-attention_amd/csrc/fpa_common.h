@@ -34,6 +34,7 @@ namespace fpa {
 typedef _Float16 f16;
 typedef f16 h8 __attribute__((ext_vector_type(8)));
 typedef f16 h4 __attribute__((ext_vector_type(4)));
+typedef f16 h2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -397,6 +398,21 @@ template <typename T, int D, int DT, int NR, int NW> struct TileLoader {
 template <typename T, int K, int DT>
 __device__ __forceinline__ f32x16 mma_p1_pad_reg(f32x16 acc, const char *tile, int row, int g, const OpRow<T, K> &breg) {
     return mma_p1_lds_reg<T, K>(acc, reinterpret_cast<const T *>(tile) + row * Pad<T, DT>::PITCH, g, breg);
+}
+
+// fp16 form of mma_p2_p3_pad with the P2 operand already converted: p2[hf] holds registers
+// 8 * hf .. 8 * hf + 7 of the accumulator tile.
+template <int DT, bool A_IS_P3>
+__device__ __forceinline__ f32x16 mma_p2h_p3_pad(f32x16 acc, const h8 (&p2)[2], const char *tile, int row0, int ncol0,
+                                                 int lane) {
+    constexpr int PITCH = Pad<f16, DT>::PITCH;
+    const f16 *X = reinterpret_cast<const f16 *>(tile) + row0 * PITCH;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+        const h8 p3 = p3_tr(X, PITCH, 16 * hf, ncol0, lane);
+        acc = A_IS_P3 ? MT<f16>::mma(p3, p2[hf], acc) : MT<f16>::mma(p2[hf], p3, acc);
+    }
+    return acc;
 }
 
 // acc += A * B with the P3 operand from a padded tile (contraction over its rows row0 .. row0 + 31,

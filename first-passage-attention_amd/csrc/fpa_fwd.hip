@@ -169,15 +169,19 @@ fpa_fwd_kernel(FwdParams p) {
         if (wave_active && s0 <= qw0 + 31) {
             const char *Kt = Ks[buf];
             const float *cA = cst[buf][0], *cP = cst[buf][1], *cPHI = cst[buf][2];
-            f32x16 s[2];
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt) s[mt] = mma_p1_pad_reg<T, D, DT>(zero16(), Kt, 32 * mt + c, g, qreg);
-
             const int jb = jt;  // BN == G: the key tile is one statistics block
-            if (jb < ib) {
-                const float Y = betal * fminf(pre_t, mid);
+            const bool diag = (jb == ib);
+            const float Y = betal * fminf(pre_t, mid);
+            const int tr = tq - s0;
+            float r = pinf();  // running min of phi over [u, t] for the in-block scan
+            // Both 32-key halves' scores first; then each half in turn (the second half's MFMAs
+            // and the first half's P V run while the other half's VALU work goes on).
+            f32x16 s[2];
+            s[1] = mma_p1_pad_reg<T, D, DT>(zero16(), Kt, 32 + c, g, qreg);
+            s[0] = mma_p1_pad_reg<T, D, DT>(zero16(), Kt, c, g, qreg);
 #pragma unroll
-                for (int mt = 0; mt < 2; ++mt)
+            for (int mt = 1; mt >= 0; --mt) {
+                if (!diag) {
 #pragma unroll
                     for (int jq = 0; jq < 4; ++jq) {
                         const int s4 = 32 * mt + 8 * jq + 4 * g;
@@ -189,15 +193,10 @@ fpa_fwd_kernel(FwdParams p) {
                             s[mt][4 * jq + e] = fmaf(s[mt][4 * jq + e], p.sc2, b2);
                         }
                     }
-            } else {
-                // Diagonal block: X_ts = min phi(s, t] inside the block.
-                const int tr = tq - s0;
-                float X[2][16];
-                float r = pinf();
-                diag_x_keys(X[1], r, cPHI, 1, tr, g);
-                diag_x_keys(X[0], r, cPHI, 0, tr, g);
-#pragma unroll
-                for (int mt = 0; mt < 2; ++mt)
+                } else {
+                    // Diagonal block: X_ts = min phi(s, t] inside the block (scan from the top).
+                    float X[16];
+                    diag_x_keys(X, r, cPHI, mt, tr, g);
 #pragma unroll
                     for (int jq = 0; jq < 4; ++jq) {
                         const int s4 = 32 * mt + 8 * jq + 4 * g;
@@ -205,48 +204,64 @@ fpa_fwd_kernel(FwdParams p) {
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const int j = 4 * jq + e, sr = s4 + e;
-                            const float bx = __builtin_amdgcn_fmed3f(0.f, fmaf(betal, X[mt][j], -p4[e]), E);
+                            const float bx = __builtin_amdgcn_fmed3f(0.f, fmaf(betal, X[j], -p4[e]), E);
                             const float b2 = (sr < tr) ? bx : 0.f;  // b_tt = 0
                             const float z = fmaf(s[mt][j], p.sc2, b2);
                             s[mt][j] = (sr > tr || s0 + sr >= p.T) ? ninf() : z;
                         }
                     }
-            }
-
-            // Online softmax (base 2); lanes c and c + 32 hold the same query.
-            float mx = ninf();
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-                for (int j = 0; j < 16; ++j) mx = fmaxf(mx, s[mt][j]);
-            mx = max_halves(mx);
-            if (__any(mx > m_i + RESCALE_SLACK)) {
-                const float m_new = fmaxf(m_i, mx);
-                const float alpha = fexp2(m_i - m_new);  // 0 on the first tile (m_i = -inf)
-                l_i *= alpha;
-#pragma unroll
-                for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-                    for (int j = 0; j < 16; ++j) oacc[dt][j] *= alpha;
-                m_i = m_new;
-            }
-            float rs = 0.f;
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    const float pv = fexp2(s[mt][j] - m_i);
-                    s[mt][j] = pv;
-                    rs += pv;
                 }
-            l_i += sum_halves(rs);
 
-            // O^T[d][t] += V^T[d][s] P^T[s][t]   (V read transposed from its natural layout)
+                // Online softmax (base 2) over these 32 keys; lanes c and c + 32 hold the same query.
+                float mx = s[mt][0];
 #pragma unroll
-            for (int dt = 0; dt < NDT; ++dt)
+                for (int j = 1; j < 16; ++j) mx = fmaxf(mx, s[mt][j]);
+                mx = max_halves(mx);
+                if (__any(mx > m_i + RESCALE_SLACK)) {
+                    const float m_new = fmaxf(m_i, mx);
+                    const float alpha = fexp2(m_i - m_new);  // 0 on the first update (m_i = -inf)
+                    l_i *= alpha;
 #pragma unroll
-                for (int mt = 0; mt < 2; ++mt)
-                    oacc[dt] = mma_p2_p3_pad<T, DT, true>(oacc[dt], s[mt], Vs[buf], 32 * mt, 32 * dt, lane);
+                    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                        for (int j = 0; j < 16; ++j) oacc[dt][j] *= alpha;
+                    m_i = m_new;
+                }
+                // A half with no valid key yet (the upper half of the diagonal block for the lower
+                // queries) leaves m_i = -inf: its scores are all -inf and exponentiate to 0.
+                const float mref = (m_i > ninf()) ? m_i : 0.f;
+                if constexpr (sizeof(T) == 2) {
+                    // P in fp16 (the MFMA operand); the row sum adds the same rounded values.
+                    h8 ph[2];
+                    float rs = 0.f;
+#pragma unroll
+                    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                        for (int e = 0; e < 8; e += 2) {
+                            const h2 pp = {(f16)fexp2(s[mt][8 * hf + e] - mref), (f16)fexp2(s[mt][8 * hf + e + 1] - mref)};
+                            ph[hf][e] = pp[0];
+                            ph[hf][e + 1] = pp[1];
+                            rs = __builtin_amdgcn_fdot2(pp, h2{(f16)1.f, (f16)1.f}, rs, false);
+                        }
+                    l_i += sum_halves(rs);
+                    // O^T[d][t] += V^T[d][s] P^T[s][t]   (V read transposed from its natural layout)
+#pragma unroll
+                    for (int dt = 0; dt < NDT; ++dt)
+                        oacc[dt] = mma_p2h_p3_pad<DT, true>(oacc[dt], ph, Vs[buf], 32 * mt, 32 * dt, lane);
+                } else {
+                    float rs = 0.f;
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) {
+                        const float pv = fexp2(s[mt][j] - mref);
+                        s[mt][j] = pv;
+                        rs += pv;
+                    }
+                    l_i += sum_halves(rs);
+#pragma unroll
+                    for (int dt = 0; dt < NDT; ++dt)
+                        oacc[dt] = mma_p2_p3_pad<T, DT, true>(oacc[dt], s[mt], Vs[buf], 32 * mt, 32 * dt, lane);
+                }
+            }
 
             if (jb < ib) mid = fminf(mid, p.state[L.bplane(BP_MIN) + (int64_t)bh * p.NB + jb]);
         }
