@@ -96,6 +96,16 @@ def test_c_abi_rejects_unaligned_rows():
     assert "16-byte aligned" in L.fpa_last_error().decode()
 
 
+def test_c_abi_rejects_huge_row_stride():
+    L = _lib.lib()
+    a = _lib.FpaFwdArgs()
+    a.B, a.H, a.T, a.D, a.dtype, a.tau = 1, 1, 16, 64, 0, 1.0
+    a.q = a.k = a.v = a.o = ctypes.c_void_p(16 * 1024)
+    a.sq[:] = a.sk[:] = a.sv[:] = a.so[:] = (1 << 26, 1 << 26, 1 << 25, 1)  # 64 rows span >= 2^31 bytes
+    assert L.fpa_fwd(a, None) == _lib.FPA_ERR_INVALID
+    assert "row stride is out of range" in L.fpa_last_error().decode()
+
+
 def test_python_validation_order_and_messages():
     q = torch.zeros(1, 2, 8, 16, dtype=torch.float16)
     phi = psi = torch.zeros(1, 2, 8)
