@@ -25,28 +25,62 @@
 
 namespace fpa {
 
-constexpr int MAXNB = 2048;
-
-__device__ __forceinline__ float block_sum_256(float x, float *red) {
-    red[threadIdx.x] = x;
-    __syncthreads();
-#pragma unroll
-    for (int o = 128; o >= 1; o >>= 1) {
-        if (threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
-        __syncthreads();
+// Maximum over an array of n values held in LDS, scanned by one wave: out[i] = max of in[i..hi)
+// (suffix) or of in(lo..i] (prefix), with elements outside [lo, hi) treated as -inf.  Each lane
+// scans a contiguous chunk; chunk maxima are combined across lanes with shuffles.
+__device__ __forceinline__ void wave_suffix_max(float *out, const float *in, int n, int hi, int lane) {
+    const int k = (n + 63) / 64, i0 = lane * k;
+    float run = ninf();
+    for (int j = min(i0 + k, n) - 1; j >= i0; --j) {
+        run = fmaxf(run, (j < hi) ? in[j] : ninf());
+        out[j] = run;
     }
-    const float r = red[0];
+    // exclusive suffix maximum of the lanes' chunk maxima
+    float x = run;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float y = __shfl_down(x, o, 64);
+        if (lane + o < 64) x = fmaxf(x, y);
+    }
+    float excl = __shfl_down(x, 1, 64);
+    if (lane == 63) excl = ninf();
+    for (int j = i0; j < min(i0 + k, n); ++j) out[j] = fmaxf(out[j], excl);
+}
+__device__ __forceinline__ void wave_prefix_max(float *out, const float *in, int n, int lo, int lane) {
+    const int k = (n + 63) / 64, i0 = lane * k;
+    float run = ninf();
+    for (int j = i0; j < min(i0 + k, n); ++j) {
+        run = fmaxf(run, (j > lo) ? in[j] : ninf());
+        out[j] = run;
+    }
+    float x = run;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float y = __shfl_up(x, o, 64);
+        if (lane >= o) x = fmaxf(x, y);
+    }
+    float excl = __shfl_up(x, 1, 64);
+    if (lane == 0) excl = ninf();
+    for (int j = i0; j < min(i0 + k, n); ++j) out[j] = fmaxf(out[j], excl);
+}
+
+// Sum of x over the 256 threads in a fixed order (every call site is reached by all threads).
+__device__ __forceinline__ float block_sum_256(float x, float *red, int w, int lane) {
+    x = wave_sum(x);
+    if (lane == 0) red[w] = x;
+    __syncthreads();
+    const float r = (red[0] + red[1]) + (red[2] + red[3]);
     __syncthreads();
     return r;
 }
 
+// Dynamic LDS: sBM, scanA, scanB, NB floats each.
 __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) {
+    extern __shared__ float dyn[];
     __shared__ float sA[G], sC[G], sc[G], sW[G], sR[G];
     __shared__ float segM[4][G], segZ[4][G], segM2[4][G], segZ2[4][G], segA[4][G], segB[4][G], pp[4][G];
-    __shared__ float sBM[MAXNB];             // max a of every block of the head
-    __shared__ float scanA[MAXNB], scanB[MAXNB];
     __shared__ float contrib[G][G + 1];      // [u][s]
-    __shared__ float red[NTHREADS];
+    __shared__ float red[4];
 
     const int U = blockIdx.x, bh = blockIdx.y, b = bh / p.H, h = bh % p.H;
     const int tid = threadIdx.x, lane = tid % 64;
@@ -57,6 +91,16 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
     const int64_t brow = (int64_t)bh * p.NB;
     const float il2 = p.il2;
     const int NB = p.NB;
+    float *sBM = dyn, *scanA = dyn + NB, *scanB = dyn + 2 * NB;
+
+    // This lane's 16 gated in-block dS values (column s = lane, rows u in [16w, 16w + 16)),
+    // loaded first so that their latency overlaps the setup below.
+    f32x4 gq[4];
+    {
+        const f32x4 *gsrc = reinterpret_cast<const f32x4 *>(p.gd + ((brow + U) * G + lane) * G + 16 * w);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) gq[i] = gsrc[i];
+    }
 
     if (U == 0 && b == 0) {  // dbeta[h] = sum over batches and key-side partials
         const int n = p.NK32;
@@ -65,7 +109,7 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
             const float *src = p.dbp + (int64_t)(bb * p.H + h) * p.NK32;
             for (int i = tid; i < n; i += NTHREADS) acc += src[i];
         }
-        const float tot = block_sum_256(acc, red);
+        const float tot = block_sum_256(acc, red, w, lane);
         if (tid == 0) p.dbeta[h] = tot;
     }
 
@@ -80,33 +124,17 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
         sW[tid] = p.wsum[r];
         sR[tid] = p.rsum[r];
     }
-    for (int i = tid; i < NB; i += NTHREADS) {
-        const float bm = -p.state[L.bplane(BP_MIN) + brow + i] * il2;
-        sBM[i] = bm;
-        scanA[i] = (i < U) ? bm : ninf();  // suffix maxima over [i, U)
-        scanB[i] = (i > U) ? bm : ninf();  // prefix maxima over (U, i]
-    }
+    for (int i = tid; i < NB; i += NTHREADS) sBM[i] = -p.state[L.bplane(BP_MIN) + brow + i] * il2;
     __syncthreads();
     const float cU = sBM[U];
     const int nI = NB - 1 - U;
     const int npairs = U * nI;
     float SU = 0.f;
-    if (npairs > 0) {
-        for (int off = 1; off < NB; off <<= 1) {  // Hillis-Steele scans in place, two phases per step
-            float va[MAXNB / NTHREADS], vb[MAXNB / NTHREADS];
-            int k = 0;
-            for (int i = tid; i < NB; i += NTHREADS, ++k) {
-                va[k] = (i + off < NB) ? fmaxf(scanA[i], scanA[i + off]) : scanA[i];
-                vb[k] = (i >= off) ? fmaxf(scanB[i], scanB[i - off]) : scanB[i];
-            }
-            __syncthreads();
-            k = 0;
-            for (int i = tid; i < NB; i += NTHREADS, ++k) {
-                scanA[i] = va[k];
-                scanB[i] = vb[k];
-            }
-            __syncthreads();
-        }
+    if (npairs > 0) {  // uniform: U is the workgroup's block
+        // scanA[i] = max over [i, U), scanB[i] = max over (U, i]; waves 0 and 1 in parallel.
+        if (w == 0) wave_suffix_max(scanA, sBM, NB, U, lane);
+        if (w == 1) wave_prefix_max(scanB, sBM, NB, U, lane);
+        __syncthreads();
         // cmid(ib, jb) = max(A_jb, c_U, B_ib), A_jb = max over (jb, U) = scanA[jb + 1],
         // B_ib = max over (U, ib) = scanB[ib - 1].  Consecutive threads read consecutive jb.
         float acc = 0.f;
@@ -116,7 +144,7 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
             const float *tb = p.tbuf + ((brow + ib) * NB + jb) * 2;
             acc += fexp2(cU - cm) * (tb[0] + tb[1]);
         }
-        SU = block_sum_256(acc, red);
+        SU = block_sum_256(acc, red, w, lane);
     }
 
     // In-block pairs.  Lane s owns column s; wave w owns the steps u in [16w, 16w + 16).
@@ -125,7 +153,6 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
     // reruns its segment from the joined state.
     {
         const int s = lane, u0 = 16 * w;
-        const float *gcol = p.gd + ((brow + U) * G + s) * G;
         float m = ninf(), Z = 0.f;
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
@@ -177,7 +204,7 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
                 const float m1 = (k < 15) ? mv[k + 1] : mnext;
                 const float z1 = (k < 15) ? zv[k + 1] : znext;
                 rho[k] = (u < last) ? zv[k] * fexp2(mv[k] - m1) * frcp(z1) : 0.f;
-                gv[k] = gcol[u];
+                gv[k] = gq[k / 4][k % 4];
                 lam = fmaf(rho[k], lam, gv[k]);
                 Bc *= rho[k];
             }
@@ -198,20 +225,25 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
             contrib[u][s] = cval;
         }
     }
+    __syncthreads();  // contrib complete
     {
-        // Key-block and query-block parts: lane u, wave w sums its 16 of the 64 terms.
+        // Key-block, query-block and in-block parts: lane u, wave w sums its 16 of the 64 terms
+        // of each.
         const int u = lane, v0 = 16 * w;
-        float part = 0.f;
+        float part = 0.f, p4 = 0.f;
         if (u <= last) {
             const float au = sA[u];
 #pragma unroll
             for (int k = 0; k < 16; ++k) {
                 const int v = v0 + k;
-                if (v < u) part = fmaf(fexp2(au - sC[v]), sW[v], part);
+                if (v < u) {
+                    part = fmaf(fexp2(au - sC[v]), sW[v], part);
+                    p4 += contrib[u][v];
+                }
                 if (v >= u && v <= last) part = fmaf(fexp2(au - sc[v]), sR[v], part);
             }
         }
-        pp[w][u] = part;
+        pp[w][u] = part + p4;
     }
     __syncthreads();
     if (w == 0) {
@@ -219,15 +251,14 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
         if (u <= last) {
             float tot = ((pp[0][u] + pp[1][u]) + (pp[2][u] + pp[3][u]));
             if (npairs > 0) tot += fexp2(sA[u] - cU) * SU;
-            float p4 = 0.f;
-            for (int s = 0; s < u; ++s) p4 += contrib[u][s];
-            p.dphi[(int64_t)bh * p.T + sb + u] = p.beta[h] * (tot + p4);
+            p.dphi[(int64_t)bh * p.T + sb + u] = p.beta[h] * tot;
         }
     }
 }
 
 hipError_t launch_bwd_combine(const BwdParams &p, hipStream_t s) {
-    hipLaunchKernelGGL(fpa_bwd_combine_kernel, dim3(p.NB, p.BH), dim3(NTHREADS), 0, s, p);
+    const size_t dyn = 3 * (size_t)p.NB * sizeof(float);
+    hipLaunchKernelGGL(fpa_bwd_combine_kernel, dim3(p.NB, p.BH), dim3(NTHREADS), dyn, s, p);
     return hipGetLastError();
 }
 
