@@ -147,11 +147,16 @@ fpa_bwd_kv_kernel(BwdParams p) {
     float mid = pinf(), midl = ninf(), cmid = ninf();  // over blocks strictly between jb and ib
     const float *phiblk = kPHI + (sb - k0);
 
+    // Block statistics used by a query block, loaded one block ahead: BMIN / BLSE of block
+    // ib - 1 (which joins the middle) and BLSE of block ib.
+    float bm_prev = 0.f, bl_prev = 0.f, bl_cur = p.state[L.bplane(BP_LSE) + brow + ib0];
     wait_loads();
     __syncthreads();
     for (int ib = ib0, it = 0; ib < p.NB; ++ib, ++it) {
         const int buf = it & 1;
         if (ib + 1 < p.NB) issue(ib + 1, buf ^ 1);
+        const float bm_here = p.state[L.bplane(BP_MIN) + brow + ib];
+        const float bl_next = (ib + 1 < p.NB) ? p.state[L.bplane(BP_LSE) + brow + ib + 1] : 0.f;
         if (wave_active && ib >= jb) {
             // Soft-min denominators off the diagonal: Z_ts 2^{-rs} = sv + 2^{PREL_t - rs} with the
             // per-key reference rs = max(C_s, cmid) (sv >= 1 when rs is finite).  With
@@ -164,14 +169,13 @@ fpa_bwd_kv_kernel(BwdParams p) {
             bool prod = false;
             if (ib > jb) {
                 if (ib - 1 > jb) {  // block ib - 1 joins the middle
-                    const float bm = p.state[L.bplane(BP_MIN) + brow + ib - 1];
-                    mid = fminf(mid, bm);
-                    midl = lse2_pair(midl, p.state[L.bplane(BP_LSE) + brow + ib - 1]);
-                    cmid = fmaxf(cmid, -bm * p.il2);
+                    mid = fminf(mid, bm_prev);
+                    midl = lse2_pair(midl, bl_prev);
+                    cmid = fmaxf(cmid, -bm_prev * p.il2);
                 }
                 rs = fmaxf(Cs, cmid);
                 sv = (rs > ninf()) ? fexp2(sufl - rs) + fexp2(midl - rs) : 0.f;
-                rsb = rs - p.state[L.bplane(BP_LSE) + brow + ib];
+                rsb = rs - bl_cur;
                 ck = fexp2(fminf(-rsb, 126.f));
                 prod = uniform_f(qi[buf][QI_ZQ][0]) > 0.f;
             }
@@ -266,6 +270,9 @@ fpa_bwd_kv_kernel(BwdParams p) {
                 }
             }
         }
+        bm_prev = bm_here;
+        bl_prev = bl_cur;
+        bl_cur = bl_next;
         wait_loads();
         __syncthreads();
     }

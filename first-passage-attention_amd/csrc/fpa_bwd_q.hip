@@ -97,26 +97,29 @@ fpa_bwd_q_kernel(BwdParams p) {
     const float a_first = -p.state[L.plane(PL_PHI) + rowbase + ibc * G] * p.il2;  // a of the block's first query
     const float c_blk = -p.state[L.bplane(BP_MIN) + brow + ibc] * p.il2;          // max a over block ib
 
+    // BMIN / BLSE of block jb + 1 (which joins the middle), loaded one block ahead.
+    float bm_prev = 0.f, bl_prev = 0.f;
     wait_loads();
     __syncthreads();
     for (int jb = jbmax, it = 0; jb >= 0; --jb, ++it) {
         const int buf = it & 1;
         const int s0 = jb * BK;
         if (jb > 0) issue(jb - 1, buf ^ 1);
+        const float bm_here = p.state[L.bplane(BP_MIN) + brow + jb];
+        const float bl_here = p.state[L.bplane(BP_LSE) + brow + jb];
         if (wave_active && jb <= ib) {
             const float *kSUF = kst[buf][0], *kPSI = kst[buf][1], *kSUFL = kst[buf][2], *kPHI = kst[buf][3];
             if (jb + 1 < ib) {  // block jb + 1 joins the middle
-                const float bm = p.state[L.bplane(BP_MIN) + brow + jb + 1];
-                mid = fminf(mid, bm);
-                midl = lse2_pair(midl, p.state[L.bplane(BP_LSE) + brow + jb + 1]);
-                cmid = fmaxf(cmid, -bm * p.il2);
+                mid = fminf(mid, bm_prev);
+                midl = lse2_pair(midl, bl_prev);
+                cmid = fmaxf(cmid, -bm_prev * p.il2);
             }
             const float mterm = fexp2(midl - ct) + prel_ct;
             // Shared reference R >= every exponent of the tile (largest C_s is at the block's first key).
             bool fast = false;
             float R = 0.f, bq = 0.f;
             if (jb < ib) {
-                const float cfirst = -p.state[L.plane(PL_SUF) + rowbase + s0] * p.il2;
+                const float cfirst = -uniform_f(kSUF[0]) * p.il2;  // SUF of the block's first key
                 R = fmaxf(fmaxf(cfirst, cmid), c_blk);
                 fast = FPA_Q_FAST && (R - fmaxf(cmid, a_first)) < FAST_SPREAD;
                 if (fast) {
@@ -194,6 +197,8 @@ fpa_bwd_q_kernel(BwdParams p) {
             }
             if (fast) racc = fmaf(fexp2(ct - R), rblk, racc);  // R_t gets 2^{c_t} sum g / Z
         }
+        bm_prev = bm_here;
+        bl_prev = bl_here;
         wait_loads();
         __syncthreads();
     }

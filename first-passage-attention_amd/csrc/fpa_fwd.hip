@@ -166,6 +166,8 @@ fpa_fwd_kernel(FwdParams p) {
         const int buf = it & 1;
         const int s0 = jt * BN;
         if (jt > 0) issue(jt - 1, buf ^ 1);
+        // Issued here, used after the tile: the load's latency hides behind the tile's work.
+        const float bmin_jt = p.state[L.bplane(BP_MIN) + (int64_t)bh * p.NB + jt];
         if (wave_active && s0 <= qw0 + 31) {
             const char *Kt = Ks[buf];
             const float *cA = cst[buf][0], *cP = cst[buf][1], *cPHI = cst[buf][2];
@@ -263,7 +265,7 @@ fpa_fwd_kernel(FwdParams p) {
                 }
             }
 
-            if (jb < ib) mid = fminf(mid, p.state[L.bplane(BP_MIN) + (int64_t)bh * p.NB + jb]);
+            if (jb < ib) mid = fminf(mid, bmin_jt);
         }
         wait_loads();
         __syncthreads();
