@@ -182,3 +182,50 @@ def test_layer_kernel_fp16_autocast(fpa):
         out.append([y.detach().float()] + list(torch.autograd.grad(loss, list(layer.parameters()))))
     for a, b in zip(*out):
         assert ((a - b).norm() / b.norm()).item() <= 5e-3
+
+
+def test_steep_drift_and_small_tau(fpa):
+    """phi with a steep downward drift and a small tau: block log-sum-exp spreads above 100
+    binades (the exact form of the key side's soft-min denominators) and query blocks far above
+    the key blocks' references (the clamped product form); fp32 for the tight tolerance."""
+    _say("[parity] B1 H2 T1500 D64 fp32 drift 0.2, tau 0.1 and 1.0")
+    for tau in (0.1, 1.0):
+        q, k, v, phi, psi, beta, do = O.make_inputs(1, 2, 1500, 64, dtype=torch.float32, seed=51, drift=0.2)
+        check(run_hip(fpa, q, k, v, phi, psi, beta, do, tau), O.fpa_grads(q, k, v, phi, psi, beta, do, tau=tau),
+              torch.float32)
+
+
+def test_cfg3_shape_head(fpa):
+    """The fp32 wide-head shape B2 H8 T4096 D128 (beta = softplus) runs whole; one head is
+    checked against the oracle at the fp32 tolerance."""
+    _say("[parity] B2 H8 T4096 D128 fp32, head (1,5)")
+    B, H, T, D = 2, 8, 4096, 128
+    q, k, v, phi, psi, beta, do = O.make_inputs(B, H, T, D, dtype=torch.float32, seed=3, psi_noise=1.0,
+                                                beta="softplus")
+    kern = run_hip(fpa, q, k, v, phi, psi, beta, do)
+    for x in kern:
+        assert torch.isfinite(x).all()
+    b, h = 1, 5
+    sl = lambda t: t[b:b + 1, h:h + 1]  # noqa: E731
+    ref = O.fpa_grads(sl(q), sl(k), sl(v), sl(phi), sl(psi), beta[h:h + 1], sl(do))
+    for name, x, r in zip(NAMES[:6], [sl(x) for x in kern[:6]], ref[:6]):
+        assert O.rel_err(x, r) <= TOL[torch.float32], (name, O.rel_err(x, r))
+
+
+def test_cfg4_shape_prefix(fpa):
+    """The long ragged shape B1 H12 T16381 D64 fp16 with phi drift -0.01 t runs whole, twice
+    with bit-identical results.  Rows t < 2048 depend only on keys s <= t, so o and dq of those
+    rows are checked against the oracle run on the 2048-long prefix of one head."""
+    _say("[parity] B1 H12 T16381 D64 fp16 drift 0.01, prefix of head 7")
+    B, H, T, D = 1, 12, 16381, 64
+    q, k, v, phi, psi, _, do = O.make_inputs(B, H, T, D, dtype=torch.float16, seed=4, psi_noise=1.0, drift=0.01)
+    beta = torch.ones(H)
+    runs = [run_hip(fpa, q, k, v, phi, psi, beta, do) for _ in range(2)]
+    assert all(torch.equal(x, y) for x, y in zip(*runs))
+    for x in runs[0]:
+        assert torch.isfinite(x).all()
+    h, P = 7, 2048
+    sl = lambda t: t[:, h:h + 1, :P]  # noqa: E731
+    ref = O.fpa_grads(sl(q), sl(k), sl(v), sl(phi), sl(psi), beta[h:h + 1], sl(do))
+    for name, idx in (("o", 0), ("dq", 1)):
+        assert O.rel_err(sl(runs[0][idx]), ref[idx]) <= TOL[torch.float16], (name, O.rel_err(sl(runs[0][idx]), ref[idx]))
