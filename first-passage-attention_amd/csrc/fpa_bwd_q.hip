@@ -35,7 +35,7 @@ fpa_bwd_q_kernel(BwdParams p) {
     constexpr int TB = Pad<T, DT>::template bytes<BK>();  // one padded K or V tile
     __shared__ __attribute__((aligned(1024))) char Ks[2][TB];
     __shared__ __attribute__((aligned(1024))) char Vs[2][TB];
-    // Per-key values of a block: SUF, PSI, SUFL, PHI.
+    // Per-key values of a block: BSUF, CP (= betal * psi), SUFL, PHI.
     __shared__ __attribute__((aligned(1024))) float kst[2][4][BK];
     __shared__ __attribute__((aligned(16))) float Aw[NW][BK];  // per-wave key factors of the shared-reference path
 
@@ -57,8 +57,8 @@ fpa_bwd_q_kernel(BwdParams p) {
     const T *Kb = static_cast<const T *>(p.k) + b * p.sk.b + h * p.sk.h;
     const T *Vb = static_cast<const T *>(p.v) + b * p.sv.b + h * p.sv.h;
     const T *DOb = static_cast<const T *>(p.dout) + b * p.sdo.b + h * p.sdo.h;
-    // lanes 0-15: SUF, 16-31: PSI, 32-47: SUFL, 48-63: PHI
-    const int kpl = (lane < 16) ? PL_SUF : (lane < 32) ? PL_PSI : (lane < 48) ? PL_SUFL : PL_PHI;
+    // lanes 0-15: BSUF, 16-31: CP, 32-47: SUFL, 48-63: PHI
+    const int kpl = (lane < 16) ? PL_BSUF : (lane < 32) ? PL_CP : (lane < 48) ? PL_SUFL : PL_PHI;
     const float *kst_src = p.state + L.plane(kpl) + rowbase + 4 * (lane & 15);
 
     TileLoader<T, D, DT, BK, NW> kld, vld;
@@ -87,6 +87,42 @@ fpa_bwd_q_kernel(BwdParams p) {
     }
     const float ct = -pre * p.il2;  // max a over [start of blk(t), t]
     const float prel_ct = fexp2(prel - ct);
+    const float E = (betal >= 0.f) ? ninf() : pinf();  // med3(x, y, E) = min (beta >= 0) or max (beta < 0)
+
+    // One more contraction step folds -lse_t into S and -Delta_t into dP: the key side's operand
+    // is {2^k, 2^k} (first two of its 16 entries), the query side's {-hi, -lo} with
+    // hi + lo = (lse / sc2) / 2^k (resp. Delta / 2^k) in fp16; k (per wave, usually 0) keeps
+    // hi within fp16 range.  fp32 operands carry the value in one entry.  Rows past T get
+    // lse = +inf, which becomes a -inf score (P = 0).
+    typename MT<T>::op_t kone_s, kone_d, qaug, daug;
+    if constexpr (sizeof(T) == 2) {
+        const f16 zero = (f16)0.f;
+        const h8 z8 = {zero, zero, zero, zero, zero, zero, zero, zero};
+        auto pow2_scale = [&](float x) {  // smallest 2^k (k <= 15) with max |x| / 2^k below 16384
+            float m = (__float_as_uint(x) & 0x7f800000u) == 0x7f800000u ? 0.f : fabsf(x);
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+            float sc = 1.f;
+            for (int k = 0; k < 15 && m >= 16384.f * sc; ++k) sc *= 2.f;
+            return uniform_f(sc);
+        };
+        auto fold = [&](float x, float sc) {
+            const float xs = x / sc;
+            const f16 hi = (f16)xs;
+            const f16 lo = ((__float_as_uint(xs) & 0x7f800000u) == 0x7f800000u) ? zero : (f16)(xs - (float)hi);
+            return h8{(f16)-hi, (f16)-lo, zero, zero, zero, zero, zero, zero};
+        };
+        const float lq = lse / p.sc2;
+        const float scl = pow2_scale(lq), scd = pow2_scale(del);
+        kone_s = g ? z8 : h8{(f16)scl, (f16)scl, zero, zero, zero, zero, zero, zero};
+        kone_d = g ? z8 : h8{(f16)scd, (f16)scd, zero, zero, zero, zero, zero, zero};
+        qaug = g ? z8 : fold(lq, scl);
+        daug = g ? z8 : fold(del, scd);
+    } else {
+        kone_s = kone_d = g ? 0.f : 1.f;
+        qaug = g ? 0.f : -lse / p.sc2;
+        daug = g ? 0.f : -del;
+    }
 
     f32x16 dqacc[NDT];
 #pragma unroll
@@ -107,6 +143,7 @@ fpa_bwd_q_kernel(BwdParams p) {
         if (jb > 0) issue(jb - 1, buf ^ 1);
         const float bm_here = p.state[L.bplane(BP_MIN) + brow + jb];
         const float bl_here = p.state[L.bplane(BP_LSE) + brow + jb];
+        const float suf_first = p.state[L.plane(PL_SUF) + rowbase + s0];
         if (wave_active && jb <= ib) {
             const float *kSUF = kst[buf][0], *kPSI = kst[buf][1], *kSUFL = kst[buf][2], *kPHI = kst[buf][3];
             if (jb + 1 < ib) {  // block jb + 1 joins the middle
@@ -119,7 +156,7 @@ fpa_bwd_q_kernel(BwdParams p) {
             bool fast = false;
             float R = 0.f, bq = 0.f;
             if (jb < ib) {
-                const float cfirst = -uniform_f(kSUF[0]) * p.il2;  // SUF of the block's first key
+                const float cfirst = -suf_first * p.il2;  // SUF of the block's first key
                 R = fmaxf(fmaxf(cfirst, cmid), c_blk);
                 fast = FPA_Q_FAST && (R - fmaxf(cmid, a_first)) < FAST_SPREAD;
                 if (fast) {
@@ -128,7 +165,7 @@ fpa_bwd_q_kernel(BwdParams p) {
                 }
             }
             float rblk = 0.f;  // sum of g / (Z 2^{-R}) over this key block (shared-reference path)
-            const float Y = fminf(pre, mid);
+            const float bY = betal * fminf(pre, mid);
             const bool diag = (jb == ib);
             const int tr = tq - s0;
             const char *Kt = Ks[buf];
@@ -136,8 +173,9 @@ fpa_bwd_q_kernel(BwdParams p) {
             float r = pinf();  // running min of phi over [u, t] for the in-block scan
 #pragma unroll 1
             for (int mt = 1; mt >= 0; --mt) {
-                f32x16 S = mma_p1_pad_reg<T, D, DT>(zero16(), Kt, 32 * mt + c, g, qreg);   // [s][t]
-                f32x16 dP = mma_p1_pad_reg<T, D, DT>(zero16(), Vt, 32 * mt + c, g, doreg);
+                // S' = S - lse_t / sc2 and dP' = dP - Delta_t  ([s][t])
+                f32x16 S = MT<T>::mma(kone_s, qaug, mma_p1_pad_reg<T, D, DT>(zero16(), Kt, 32 * mt + c, g, qreg));
+                f32x16 dP = MT<T>::mma(kone_d, daug, mma_p1_pad_reg<T, D, DT>(zero16(), Vt, 32 * mt + c, g, doreg));
                 float X[16];
                 if (diag) diag_x_keys(X, r, kPHI, mt, tr, g);  // X_ts = min phi(s, t] in the block
                 if (!diag) {
@@ -147,18 +185,20 @@ fpa_bwd_q_kernel(BwdParams p) {
 #pragma unroll
                         for (int jq = 0; jq < 4; ++jq) {
                             const int s4 = 32 * mt + 8 * jq + 4 * g;
-                            const f32x4 suf4 = *reinterpret_cast<const f32x4 *>(&kSUF[s4]);
-                            const f32x4 psi4 = *reinterpret_cast<const f32x4 *>(&kPSI[s4]);
+                            const f32x4 bsuf4 = *reinterpret_cast<const f32x4 *>(&kSUF[s4]);
+                            const f32x4 bpsi4 = *reinterpret_cast<const f32x4 *>(&kPSI[s4]);
                             const f32x4 zk4 = FAST ? *reinterpret_cast<const f32x4 *>(&Aw[w][s4])
                                                    : *reinterpret_cast<const f32x4 *>(&kSUFL[s4]);
 #pragma unroll
                             for (int e = 0; e < 4; ++e) {
                                 const int j = 4 * jq + e;
-                                const float x = fminf(suf4[e], Y) - psi4[e];  // min(SUF_s, MID, PRE_t) - psi_s
-                                const float xm = fminf(x, 0.f);
-                                const float P = fexp2(fmaf(S[j], p.sc2, fmaf(betal, xm, -lse)));
-                                const float dS = P * (dP[j] - del);
-                                const float gg = (x <= 0.f) ? dS : 0.f;
+                                // v = betal * x with x = min(SUF_s, MID, PRE_t) - psi_s, and the bias
+                                // bm = betal * min(x, 0); the gate x <= 0 is bm == v for either sign.
+                                const float v = __builtin_amdgcn_fmed3f(bsuf4[e], bY, E) - bpsi4[e];
+                                const float bm = __builtin_amdgcn_fmed3f(v, 0.f, E);
+                                const float P = fexp2(fmaf(S[j], p.sc2, bm));
+                                const float dS = P * dP[j];
+                                const float gg = (bm == v) ? dS : 0.f;
                                 if constexpr (FAST)
                                     rblk = fmaf(gg, frcp(zk4[e] + bq), rblk);
                                 else
@@ -177,16 +217,16 @@ fpa_bwd_q_kernel(BwdParams p) {
 #pragma unroll
                     for (int jq = 0; jq < 4; ++jq) {
                         const int s4 = 32 * mt + 8 * jq + 4 * g;
-                        const f32x4 psi4 = *reinterpret_cast<const f32x4 *>(&kPSI[s4]);
+                        const f32x4 bpsi4 = *reinterpret_cast<const f32x4 *>(&kPSI[s4]);
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const int j = 4 * jq + e;
                             const int s = s0 + s4 + e;
                             const bool valid = t_valid && (s <= tq);
                             const bool strict = valid && (s < tq);
-                            const float xm = strict ? fminf(X[j] - psi4[e], 0.f) : 0.f;
-                            const float P = valid ? fexp2(fmaf(S[j], p.sc2, fmaf(betal, xm, -lse))) : 0.f;
-                            S[j] = P * (dP[j] - del);
+                            const float bm = strict ? __builtin_amdgcn_fmed3f(fmaf(betal, X[j], -bpsi4[e]), 0.f, E) : 0.f;
+                            const float P = valid ? fexp2(fmaf(S[j], p.sc2, bm)) : 0.f;
+                            S[j] = P * dP[j];
                         }
                     }
                 }

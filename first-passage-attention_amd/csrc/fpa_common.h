@@ -500,14 +500,16 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 
 // State planes (float offsets), each plane is BH * TP floats except the two block planes.
+constexpr int NPL = 9;  // per-position planes
 struct StateLayout {
     int64_t BH, TP, NB;
-    __host__ __device__ int64_t plane(int k) const { return (int64_t)k * BH * TP; }  // 0..7
-    __host__ __device__ int64_t bplane(int k) const { return 8 * BH * TP + (int64_t)k * BH * NB; }  // 0..1
-    __host__ __device__ int64_t total() const { return 8 * BH * TP + 2 * BH * NB; }
+    __host__ __device__ int64_t plane(int k) const { return (int64_t)k * BH * TP; }  // 0 .. NPL-1
+    __host__ __device__ int64_t bplane(int k) const { return NPL * BH * TP + (int64_t)k * BH * NB; }  // 0..1
+    __host__ __device__ int64_t total() const { return NPL * BH * TP + 2 * BH * NB; }
 };
-// PL_CA = beta*log2e*min(SUF - psi, 0) and PL_CP = beta*log2e*psi: the forward's per-key bias terms.
-enum { PL_PHI = 0, PL_PSI = 1, PL_PRE = 2, PL_PREL = 3, PL_SUF = 4, PL_SUFL = 5, PL_CA = 6, PL_CP = 7 };
+// Per-key bias terms, betal = beta * log2(e): PL_CA = betal * min(SUF - psi, 0), PL_CP = betal * psi,
+// PL_BSUF = betal * SUF (an infinite SUF keeps the sign of beta, and gives 0 when beta = 0).
+enum { PL_PHI = 0, PL_PSI = 1, PL_PRE = 2, PL_PREL = 3, PL_SUF = 4, PL_SUFL = 5, PL_CA = 6, PL_CP = 7, PL_BSUF = 8 };
 enum { BP_MIN = 0, BP_LSE = 1 };
 
 }  // namespace fpa

@@ -27,6 +27,7 @@ namespace fpa {
 //   SUF_s     = min phi(s .. eb)           SUFL_s = log2 sum 2^a(s .. eb)
 //   BMIN, BLSE: the whole block.           a_u = -phi_u * log2(e) / tau
 //   CA, CP    : beta*log2e*min(SUF - psi, 0) and beta*log2e*psi (the forward's per-key terms)
+//   BSUF      : beta*log2e*SUF (the query side's per-key term)
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(64) fpa_stats_kernel(StatsParams p) {
     const int blk = blockIdx.x, bh = blockIdx.y;
@@ -76,6 +77,7 @@ __global__ void __launch_bounds__(64) fpa_stats_kernel(StatsParams p) {
     const float betal = p.beta[bh % p.H] * LOG2E;
     p.state[L.plane(PL_CA) + r] = betal * fminf(suf - ps, 0.f);
     p.state[L.plane(PL_CP) + r] = betal * ps;
+    p.state[L.plane(PL_BSUF) + r] = (suf < pinf()) ? betal * suf : (betal > 0.f ? pinf() : betal < 0.f ? ninf() : 0.f);
     if (lane == 63) {
         p.state[L.bplane(BP_MIN) + (int64_t)bh * p.NB + blk] = pm;
         p.state[L.bplane(BP_LSE) + (int64_t)bh * p.NB + blk] = pl;
