@@ -29,13 +29,30 @@
 namespace fpa {
 
 // Per-query planes of the backward (QI_*), for t < TP:
-//   LSE   lse_t (+inf past T: P = 0 there with no per-element mask)
-//   DEL   Delta_t = sum_d dO_td O_td (0 past T)
-//   PRE   PRE_t (+inf past T)
+//   L, D  the key side's extra contraction step that subtracts lse_t / sc2 from S and Delta_t from
+//         dP on the MFMA: with the key-side operand {2048, 1, 1} (fp16) the query-side operand is
+//         {-a, -b, -c}, a = fp16(rint(x / 2048)), b = fp16(x - 2048 a), c = fp16(x - 2048 a - b)
+//         (x = lse_t / sc2 resp. Delta_t; |x| < 1.3e8); fp32 keys take {1} and {-x}.  Rows past T
+//         get a = 65504 (fp16) or x = 1e30 (fp32): their scores become hugely negative and P = 0
+//         there with no per-element mask.  Delta_t = sum_d dO_td O_td (0 past T).
+//   BPRE  beff * PRE_t (beff = beta * log2e, or 2^-100 for beta = 0; +-inf past T)
 //   ZQ    with PRL_t = PREL_t - BLSE <= 0 (BLSE = log2 sum 2^a over t's block; 0 past T):
 //         2^{PRL_t} > 0 when the block's spread -PRL_{first row} is at most PROD_SPREAD
 //         (product form of the soft-min denominators), else PRL_t <= 0 (exact form).  The sign
 //         of the block's first entry tells the two apart.
+//   DEL   Delta_t in fp32 (the query side's operand).
+__device__ __forceinline__ float beta_eff(float betal) { return betal != 0.f ? betal : 0x1p-100f; }
+
+// Three fp16 terms x = 2048 a + b + c (see QI_L), negated and packed as two 32-bit words.
+__device__ __forceinline__ void fold_terms(float x, float &w0, float &w1) {
+    const f16 a = (f16)fminf(fmaxf(rintf(x * (1.f / 2048.f)), -65504.f), 65504.f);
+    const float r = x - 2048.f * (float)a;
+    const f16 bb = (f16)r, cc = (f16)(r - (float)bb);
+    const h2 v0 = {(f16)-a, (f16)-bb}, v1 = {(f16)-cc, (f16)0.f};
+    w0 = __builtin_bit_cast(float, v0);
+    w1 = __builtin_bit_cast(float, v1);
+}
+
 template <typename T, int D>
 __global__ void __launch_bounds__(NTHREADS) fpa_bwd_prep_kernel(BwdParams p) {
     constexpr int CE = MT<T>::CHUNK;
@@ -69,10 +86,28 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_prep_kernel(BwdParams p) {
         const float blse = p.state[L.bplane(BP_LSE) + (int64_t)bh * p.NB + row / G];
         const float prl = ok ? p.state[L.plane(PL_PREL) + r] - blse : 0.f;
         const float spread = blse - p.state[L.plane(PL_PREL) + (int64_t)bh * p.TP + (row / G) * G];
-        p.qinfo[QI_LSE * QP + r] = ok ? p.lse[r] : pinf();
-        p.qinfo[QI_DEL * QP + r] = ok ? acc : 0.f;
-        p.qinfo[QI_PRE * QP + r] = ok ? p.state[L.plane(PL_PRE) + r] : pinf();
+        const float beff = beta_eff(p.beta[bh % p.H] * LOG2E);
+        const float del = ok ? acc : 0.f;
+        float l0, l1, d0, d1;
+        if constexpr (sizeof(T) == 2) {
+            if (ok) {
+                fold_terms(p.lse[r] / p.sc2, l0, l1);
+            } else {
+                const h2 big = {(f16)-65504.f, (f16)0.f};
+                l0 = __builtin_bit_cast(float, big);
+                l1 = 0.f;
+            }
+            fold_terms(del, d0, d1);
+        } else {
+            l0 = ok ? -p.lse[r] / p.sc2 : -1e30f;
+            d0 = -del;
+            l1 = d1 = 0.f;
+        }
+        *reinterpret_cast<f32x2 *>(&p.qinfo[QI_L * QP + 2 * r]) = f32x2{l0, l1};
+        *reinterpret_cast<f32x2 *>(&p.qinfo[QI_D * QP + 2 * r]) = f32x2{d0, d1};
+        p.qinfo[QI_BPRE * QP + r] = beff * (ok ? p.state[L.plane(PL_PRE) + r] : pinf());
         p.qinfo[QI_ZQ * QP + r] = (FPA_KV_PROD && spread <= PROD_SPREAD) ? fexp2(prl) : prl;
+        p.qinfo[QI_DEL * QP + r] = del;
     }
 }
 
@@ -85,8 +120,9 @@ fpa_bwd_kv_kernel(BwdParams p) {
     constexpr int TB = Pad<T, DT>::template bytes<BQ>();  // one padded Q or dO tile
     __shared__ __attribute__((aligned(1024))) char Qs[2][TB];
     __shared__ __attribute__((aligned(1024))) char dOs[2][TB];
-    // Per-query planes of a block: QI_LSE, QI_DEL, QI_PRE, QI_ZQ.
-    __shared__ __attribute__((aligned(1024))) float qi[2][QI_N][BQ];
+    // Per-query values of a block: planes 0-1 the L pairs, 2-3 the D pairs, 4 BPRE, 5 ZQ (6-7 copies
+    // of 4-5 that fill the second load instruction).
+    __shared__ __attribute__((aligned(1024))) float qi[2][8][BQ];
     __shared__ __attribute__((aligned(16))) float kPHI[BK];
 
     const int tid = threadIdx.x, lane = tid % 64, g = lane / 32, c = lane % 32;
@@ -108,8 +144,9 @@ fpa_bwd_kv_kernel(BwdParams p) {
     const T *Kb = static_cast<const T *>(p.k) + b * p.sk.b + h * p.sk.h;
     const T *Vb = static_cast<const T *>(p.v) + b * p.sv.b + h * p.sv.h;
     const T *DOb = static_cast<const T *>(p.dout) + b * p.sdo.b + h * p.sdo.h;
-    // lanes 0-15: LSE, 16-31: DEL, 32-47: PRE, 48-63: ZQ
-    const float *qi_src = p.qinfo + (lane >> 4) * QP + rowbase + 4 * (lane & 15);
+    // First load: lanes 0-31 the L pairs, 32-63 the D pairs; second: BPRE, ZQ, BPRE, ZQ.
+    const float *qa_src = p.qinfo + ((lane < 32) ? QI_L : QI_D) * QP + 2 * rowbase + 4 * (lane & 31);
+    const float *qb_src = p.qinfo + (QI_BPRE + ((lane >> 4) & 1)) * QP + rowbase + 4 * (lane & 15);
 
     TileLoader<T, D, DT, BQ, NW> qld, dld;
     qld.init(p.sq.t, w, lane);
@@ -117,7 +154,8 @@ fpa_bwd_kv_kernel(BwdParams p) {
     auto issue = [&](int ib, int buf) {
         qld.issue(Qs[buf], Qb, p.sq.t, ib * BQ, p.T, w, lane);
         dld.issue(dOs[buf], DOb, p.sdo.t, ib * BQ, p.T, w, lane);
-        if (w == NW - 1) gl_lds16(qi_src + ib * BQ, &qi[buf][0][0]);
+        if (w == NW - 1) gl_lds16(qa_src + 2 * ib * BQ, &qi[buf][0][0]);
+        if (w == (NW >= 2 ? NW - 2 : 0)) gl_lds16(qb_src + ib * BQ, &qi[buf][4][0]);
     };
     const int ib0 = k0 / G;
     issue(ib0, 0);
@@ -126,7 +164,11 @@ fpa_bwd_kv_kernel(BwdParams p) {
     load_row_p1<T, D>(kreg, Kb + (int64_t)s * p.sk.t, s_valid, g);
     load_row_p1<T, D>(vreg, Vb + (int64_t)s * p.sv.t, s_valid, g);
 
-    const float beta = p.beta[h], betal = beta * LOG2E;
+    // Bias terms scaled by beff = beta * log2e (2^-100 for beta = 0, below fp32 resolution in the
+    // exponent): v = beff * x with x = min(SUF_s, MID, PRE_t) - psi_s, bm = beff * min(x, 0) =
+    // med3(v, 0, E), and the gate x <= 0 is bm == v for either sign of beta.
+    const float beta = p.beta[h], beff = beta_eff(beta * LOG2E);
+    const float E = (beff > 0.f) ? ninf() : pinf();  // med3(x, y, E) = min (beff > 0) or max
     float psi_s = 0.f, suf = pinf(), sufl = ninf();
     if (s < p.TP) {
         psi_s = p.state[L.plane(PL_PSI) + rowbase + s];
@@ -134,7 +176,23 @@ fpa_bwd_kv_kernel(BwdParams p) {
         sufl = p.state[L.plane(PL_SUFL) + rowbase + s];
     }
     const float Cs = (suf < pinf()) ? -suf * p.il2 : ninf();  // max a over (s, end of block)
-    const float sufpsi = suf - psi_s;
+    const float bsuf = beff * suf, bpsi = beff * psi_s;
+    // The key side's operand of the extra contraction step (see QI_L): {2048, 1, 1} / {1}.
+    typename MT<T>::op_t kone;
+    if constexpr (sizeof(T) == 2) {
+        const f16 z = (f16)0.f, o = (f16)1.f;
+        kone = g ? h8{z, z, z, z, z, z, z, z} : h8{(f16)2048.f, o, o, z, z, z, z, z};
+    } else {
+        kone = g ? 0.f : 1.f;
+    }
+    // Query-side operand of row `row` from a pair plane of the staged block.
+    auto aug_op = [&](const float *pairs, int row) {
+        const f32x2 v = *reinterpret_cast<const f32x2 *>(&pairs[2 * row]);
+        if constexpr (sizeof(T) == 2)
+            return __builtin_bit_cast(h8, f32x4{v[0], v[1], 0.f, 0.f});
+        else
+            return v[0];
+    };
     if (tid < BK) kPHI[tid] = (k0 + tid < p.TP) ? p.state[L.plane(PL_PHI) + rowbase + k0 + tid] : pinf();
 
     f32x16 dkacc[NDT], dvacc[NDT];
@@ -179,10 +237,10 @@ fpa_bwd_kv_kernel(BwdParams p) {
                 ck = fexp2(fminf(-rsb, 126.f));
                 prod = uniform_f(qi[buf][QI_ZQ][0]) > 0.f;
             }
-            const float Ap = fminf(sufpsi, mid - psi_s);  // min(SUF_s, MID) - psi_s
+            const float cA = __builtin_amdgcn_fmed3f(bsuf, beff * mid, E);  // beff * min(SUF_s, MID)
             const char *Qt = Qs[buf];
             const char *Dt = dOs[buf];
-            const float *rLSE = qi[buf][QI_LSE], *rDEL = qi[buf][QI_DEL], *rPRE = qi[buf][QI_PRE];
+            const float *rBPRE = qi[buf][4];
             const bool diag = (ib == jb);
             const int sr = s - sb;
             float r = pinf();  // running min of phi over (s, u] for the in-block scan
@@ -190,8 +248,11 @@ fpa_bwd_kv_kernel(BwdParams p) {
 #pragma unroll 1
             for (int mt = 0; mt < 2; ++mt) {
                 f32x16 S, dP;
-                S = mma_p1_pad_reg<T, D, DT>(zero16(), Qt, 32 * mt + c, g, kreg);   // [t][s]
-                dP = mma_p1_pad_reg<T, D, DT>(zero16(), Dt, 32 * mt + c, g, vreg);
+                // S - lse / sc2 and dP - Delta, rows t, columns s
+                S = MT<T>::mma(aug_op(qi[buf][0], 32 * mt + c), kone,
+                               mma_p1_pad_reg<T, D, DT>(zero16(), Qt, 32 * mt + c, g, kreg));
+                dP = MT<T>::mma(aug_op(qi[buf][2], 32 * mt + c), kone,
+                                mma_p1_pad_reg<T, D, DT>(zero16(), Dt, 32 * mt + c, g, vreg));
                 float X[16];
                 if (diag) diag_x_queries(X, r, phiblk, mt, sr, g);  // X_ts = min phi(s, t] in the block
                 if (!diag) {
@@ -199,24 +260,22 @@ fpa_bwd_kv_kernel(BwdParams p) {
                     // every key; rows of a ragged last block are past T and have P = 0.
                     auto offdiag = [&](auto prod_c) {
                         constexpr bool PROD = decltype(prod_c)::value;
-                        const float *rZQ = qi[buf][QI_ZQ];
+                        const float *rZQ = qi[buf][5];
 #pragma unroll
                         for (int jq = 0; jq < 4; ++jq) {
                             const int t4 = 32 * mt + 8 * jq + 4 * g;
-                            const f32x4 lse4 = *reinterpret_cast<const f32x4 *>(&rLSE[t4]);
-                            const f32x4 del4 = *reinterpret_cast<const f32x4 *>(&rDEL[t4]);
-                            const f32x4 pre4 = *reinterpret_cast<const f32x4 *>(&rPRE[t4]);
+                            const f32x4 bpre4 = *reinterpret_cast<const f32x4 *>(&rBPRE[t4]);
                             const f32x4 zq4 = *reinterpret_cast<const f32x4 *>(&rZQ[t4]);
 #pragma unroll
                             for (int e = 0; e < 4; ++e) {
                                 const int j = 4 * jq + e;
-                                const float x = fminf(Ap, pre4[e] - psi_s);  // min(SUF_s, MID, PRE_t) - psi_s
-                                const float xm = fminf(x, 0.f);
-                                const float P = fexp2(fmaf(S[j], p.sc2, fmaf(betal, xm, -lse4[e])));
-                                const float dS = P * (dP[j] - del4[e]);
-                                const float gg = (x <= 0.f) ? dS : 0.f;
+                                const float v = __builtin_amdgcn_fmed3f(cA, bpre4[e], E) - bpsi;
+                                const float bm = __builtin_amdgcn_fmed3f(v, 0.f, E);
+                                const float P = fexp2(fmaf(S[j], p.sc2, bm));
+                                const float dS = P * dP[j];
+                                const float gg = (bm == v) ? dS : 0.f;
                                 gsum += gg;
-                                dbacc = fmaf(dS, xm, dbacc);
+                                dbacc = fmaf(dS, bm, dbacc);
                                 const float z = PROD ? fmaf(zq4[e], ck, sv) : sv + fexp2(zq4[e] - rsb);
                                 wblk = fmaf(gg, frcp(z), wblk);
                                 S[j] = P;
@@ -232,8 +291,6 @@ fpa_bwd_kv_kernel(BwdParams p) {
 #pragma unroll
                     for (int jq = 0; jq < 4; ++jq) {
                         const int t4 = 32 * mt + 8 * jq + 4 * g;
-                        const f32x4 lse4 = *reinterpret_cast<const f32x4 *>(&rLSE[t4]);
-                        const f32x4 del4 = *reinterpret_cast<const f32x4 *>(&rDEL[t4]);
                         f32x4 g4;
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
@@ -242,12 +299,12 @@ fpa_bwd_kv_kernel(BwdParams p) {
                             const bool valid = (t >= s) && s_valid;  // rows past T: lse = +inf gives P = 0
                             const bool strict = valid && (t > s);
                             const float x = X[j] - psi_s;
-                            const float xm = strict ? fminf(x, 0.f) : 0.f;
-                            const float P = valid ? fexp2(fmaf(S[j], p.sc2, fmaf(betal, xm, -lse4[e]))) : 0.f;
-                            const float dS = P * (dP[j] - del4[e]);
+                            const float bm = strict ? beff * fminf(x, 0.f) : 0.f;  // x is +inf where the range is empty
+                            const float P = valid ? fexp2(fmaf(S[j], p.sc2, bm)) : 0.f;
+                            const float dS = P * dP[j];
                             const float gg = (strict && x <= 0.f) ? dS : 0.f;
                             gsum += gg;
-                            dbacc = fmaf(dS, xm, dbacc);  // x is +inf where the range is empty
+                            dbacc = fmaf(dS, bm, dbacc);
                             g4[e] = gg;
                             S[j] = P;
                             dP[j] = dS;
@@ -280,7 +337,7 @@ fpa_bwd_kv_kernel(BwdParams p) {
     // Per-key outputs (lanes c and c + 32 hold the same key, different queries).
     gsum = sum_halves(gsum);
     Wacc = sum_halves(Wacc);
-    const float dbw = wave_sum(dbacc);
+    const float dbw = wave_sum(dbacc) / beff;
     if (!wave_active) return;
     if (lane == 0) p.dbp[(int64_t)bh * p.NK32 + kw0 / 32] = dbw;  // one partial per 32-key group
     if (g == 0 && s < p.TP) p.wsum[rowbase + s] = Wacc;

@@ -37,6 +37,7 @@ typedef f16 h4 __attribute__((ext_vector_type(4)));
 typedef f16 h2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr int G = 64;        // statistics block

@@ -61,8 +61,9 @@ struct BwdParams {
     float il2;     // log2(e) / tau
 };
 
-// Planes of BwdParams::qinfo.
-enum { QI_LSE = 0, QI_DEL = 1, QI_PRE = 2, QI_ZQ = 3, QI_N = 4 };
+// Planes of BwdParams::qinfo (each BH * TP floats).  QI_L and QI_D span two planes: row r's
+// pair of 32-bit words sits at 2 r (the key side's folded log-sum-exp and Delta operands).
+enum { QI_L = 0, QI_D = 2, QI_BPRE = 4, QI_ZQ = 5, QI_DEL = 6, QI_N = 7 };
 
 // Launchers (defined next to their kernels); return hipSuccess or the launch error.
 hipError_t launch_stats(const StatsParams &p, hipStream_t s);
