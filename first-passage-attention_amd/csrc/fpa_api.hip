@@ -33,7 +33,7 @@ WsLayout ws_layout(int64_t B, int64_t H, int64_t T) {
     const int64_t BH = B * H, TP = tp_of(T), NB = TP / G, NK32 = (T + 31) / 32;
     WsLayout w;
     int64_t off = 0;
-    w.qinfo = off; off += align64(QI_N * BH * TP);
+    w.qinfo = off; off += align64((int64_t)QI_PLANES * BH * TP);
     w.wsum = off;  off += align64(BH * TP);
     w.rsum = off;  off += align64(BH * TP);
     w.gd = off;    off += align64(BH * NB * G * G);
@@ -166,7 +166,7 @@ int fpa_bwd(const FpaBwdArgs *a, void *stream) {
     p.dv = a->dv; p.sdv = s3(a->sdv);
     p.beta = a->beta; p.lse = a->lse; p.state = a->state;
     p.dphi = a->dphi; p.dpsi = a->dpsi; p.dbeta = a->dbeta;
-    p.qinfo = ws + wl.qinfo; p.delta = p.qinfo + QI_DEL * (a->B * a->H) * TP;
+    p.qinfo = ws + wl.qinfo;
     p.wsum = ws + wl.wsum; p.rsum = ws + wl.rsum;
     p.gd = ws + wl.gd; p.tbuf = ws + wl.tbuf; p.dbp = ws + wl.dbp;
     p.B = (int)a->B; p.H = (int)a->H; p.T = (int)a->T; p.TP = (int)TP; p.NB = (int)(TP / G);

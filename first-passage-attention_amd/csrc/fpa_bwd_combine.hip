@@ -115,9 +115,9 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
 
     if (tid < G) {
         const int64_t r = rowbase + sb + tid;
-        const float ph = p.state[L.plane(PL_PHI) + r];
-        const float suf = p.state[L.plane(PL_SUF) + r];
-        const float pre = p.state[L.plane(PL_PRE) + r];
+        const float ph = p.state[L.at(PL_PHI, bh, sb + tid)];
+        const float suf = p.state[L.at(PL_SUF, bh, sb + tid)];
+        const float pre = p.state[L.at(PL_PRE, bh, sb + tid)];
         sA[tid] = (ph < pinf()) ? -ph * il2 : ninf();
         sC[tid] = (suf < pinf()) ? -suf * il2 : ninf();
         sc[tid] = (pre < pinf()) ? -pre * il2 : ninf();

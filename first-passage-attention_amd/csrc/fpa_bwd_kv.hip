@@ -81,11 +81,11 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_prep_kernel(BwdParams p) {
     acc += __shfl_xor(acc, 2, 64);
     if (part == 0 && row < p.TP) {
         const StateLayout L{p.BH, p.TP, p.NB};
-        const int64_t r = (int64_t)bh * p.TP + row, QP = (int64_t)p.BH * p.TP;
+        const int64_t r = (int64_t)bh * p.TP + row;
         const bool ok = row < p.T;
         const float blse = p.state[L.bplane(BP_LSE) + (int64_t)bh * p.NB + row / G];
-        const float prl = ok ? p.state[L.plane(PL_PREL) + r] - blse : 0.f;
-        const float spread = blse - p.state[L.plane(PL_PREL) + (int64_t)bh * p.TP + (row / G) * G];
+        const float prl = ok ? p.state[L.at(PL_PREL, bh, row)] - blse : 0.f;
+        const float spread = blse - p.state[L.at(PL_PREL, bh, (row / G) * G)];
         const float beff = beta_eff(p.beta[bh % p.H] * LOG2E);
         const float del = ok ? acc : 0.f;
         float l0, l1, d0, d1;
@@ -103,11 +103,11 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_prep_kernel(BwdParams p) {
             d0 = -del;
             l1 = d1 = 0.f;
         }
-        *reinterpret_cast<f32x2 *>(&p.qinfo[QI_L * QP + 2 * r]) = f32x2{l0, l1};
-        *reinterpret_cast<f32x2 *>(&p.qinfo[QI_D * QP + 2 * r]) = f32x2{d0, d1};
-        p.qinfo[QI_BPRE * QP + r] = beff * (ok ? p.state[L.plane(PL_PRE) + r] : pinf());
-        p.qinfo[QI_ZQ * QP + r] = (FPA_KV_PROD && spread <= PROD_SPREAD) ? fexp2(prl) : prl;
-        p.qinfo[QI_DEL * QP + r] = del;
+        *reinterpret_cast<f32x2 *>(&p.qinfo[qi_pair_at(bh, p.NB, row, QI_L)]) = f32x2{l0, l1};
+        *reinterpret_cast<f32x2 *>(&p.qinfo[qi_pair_at(bh, p.NB, row, QI_D)]) = f32x2{d0, d1};
+        p.qinfo[qi_at(bh, p.NB, row, QI_BPRE)] = beff * (ok ? p.state[L.at(PL_PRE, bh, row)] : pinf());
+        p.qinfo[qi_at(bh, p.NB, row, QI_ZQ)] = (FPA_KV_PROD && spread <= PROD_SPREAD) ? fexp2(prl) : prl;
+        p.qinfo[qi_at(bh, p.NB, row, QI_DEL)] = del;
     }
 }
 
@@ -138,15 +138,14 @@ fpa_bwd_kv_kernel(BwdParams p) {
     const StateLayout L{p.BH, p.TP, p.NB};
     const int64_t rowbase = (int64_t)bh * p.TP;
     const int64_t brow = (int64_t)bh * p.NB;
-    const int64_t QP = (int64_t)p.BH * p.TP;
 
     const T *Qb = static_cast<const T *>(p.q) + b * p.sq.b + h * p.sq.h;
     const T *Kb = static_cast<const T *>(p.k) + b * p.sk.b + h * p.sk.h;
     const T *Vb = static_cast<const T *>(p.v) + b * p.sv.b + h * p.sv.h;
     const T *DOb = static_cast<const T *>(p.dout) + b * p.sdo.b + h * p.sdo.h;
-    // First load: lanes 0-31 the L pairs, 32-63 the D pairs; second: BPRE, ZQ, BPRE, ZQ.
-    const float *qa_src = p.qinfo + ((lane < 32) ? QI_L : QI_D) * QP + 2 * rowbase + 4 * (lane & 31);
-    const float *qb_src = p.qinfo + (QI_BPRE + ((lane >> 4) & 1)) * QP + rowbase + 4 * (lane & 15);
+    // A block's per-query values: planes 0-3 (L and D pairs) and 4-7 (BPRE, ZQ, DEL, spare), one
+    // 1 KB load each.
+    const float *qi_head = p.qinfo + qi_at(bh, p.NB, 0, 0);
 
     TileLoader<T, D, DT, BQ, NW> qld, dld;
     qld.init(p.sq.t, w, lane);
@@ -154,8 +153,9 @@ fpa_bwd_kv_kernel(BwdParams p) {
     auto issue = [&](int ib, int buf) {
         qld.issue(Qs[buf], Qb, p.sq.t, ib * BQ, p.T, w, lane);
         dld.issue(dOs[buf], DOb, p.sdo.t, ib * BQ, p.T, w, lane);
-        if (w == NW - 1) gl_lds16(qa_src + 2 * ib * BQ, &qi[buf][0][0]);
-        if (w == (NW >= 2 ? NW - 2 : 0)) gl_lds16(qb_src + ib * BQ, &qi[buf][4][0]);
+        if (w == NW - 1) buf_lds16(buf_rsrc(qi_head + (int64_t)ib * QI_PLANES * 64), 16 * lane, &qi[buf][0][0]);
+        if (w == (NW >= 2 ? NW - 2 : 0))
+            buf_lds16(buf_rsrc(qi_head + (int64_t)ib * QI_PLANES * 64), 1024 + 16 * lane, &qi[buf][4][0]);
     };
     const int ib0 = k0 / G;
     issue(ib0, 0);
@@ -171,9 +171,9 @@ fpa_bwd_kv_kernel(BwdParams p) {
     const float E = (beff > 0.f) ? ninf() : pinf();  // med3(x, y, E) = min (beff > 0) or max
     float psi_s = 0.f, suf = pinf(), sufl = ninf();
     if (s < p.TP) {
-        psi_s = p.state[L.plane(PL_PSI) + rowbase + s];
-        suf = p.state[L.plane(PL_SUF) + rowbase + s];
-        sufl = p.state[L.plane(PL_SUFL) + rowbase + s];
+        psi_s = p.state[L.at(PL_PSI, bh, s)];
+        suf = p.state[L.at(PL_SUF, bh, s)];
+        sufl = p.state[L.at(PL_SUFL, bh, s)];
     }
     const float Cs = (suf < pinf()) ? -suf * p.il2 : ninf();  // max a over (s, end of block)
     const float bsuf = beff * suf, bpsi = beff * psi_s;
@@ -193,7 +193,7 @@ fpa_bwd_kv_kernel(BwdParams p) {
         else
             return v[0];
     };
-    if (tid < BK) kPHI[tid] = (k0 + tid < p.TP) ? p.state[L.plane(PL_PHI) + rowbase + k0 + tid] : pinf();
+    if (tid < BK) kPHI[tid] = (k0 + tid < p.TP) ? p.state[L.at(PL_PHI, bh, k0 + tid)] : pinf();
 
     f32x16 dkacc[NDT], dvacc[NDT];
 #pragma unroll
@@ -207,14 +207,14 @@ fpa_bwd_kv_kernel(BwdParams p) {
 
     // Block statistics used by a query block, loaded one block ahead: BMIN / BLSE of block
     // ib - 1 (which joins the middle) and BLSE of block ib.
-    float bm_prev = 0.f, bl_prev = 0.f, bl_cur = p.state[L.bplane(BP_LSE) + brow + ib0];
+    float bm_prev = 0.f, bl_prev = 0.f, bl_cur = ld_uniform(p.state, L.bplane(BP_LSE) + brow + ib0);
     wait_loads();
     __syncthreads();
     for (int ib = ib0, it = 0; ib < p.NB; ++ib, ++it) {
         const int buf = it & 1;
         if (ib + 1 < p.NB) issue(ib + 1, buf ^ 1);
-        const float bm_here = p.state[L.bplane(BP_MIN) + brow + ib];
-        const float bl_next = (ib + 1 < p.NB) ? p.state[L.bplane(BP_LSE) + brow + ib + 1] : 0.f;
+        const float bm_here = ld_uniform(p.state, L.bplane(BP_MIN) + brow + ib);
+        const float bl_next = (ib + 1 < p.NB) ? ld_uniform(p.state, L.bplane(BP_LSE) + brow + ib + 1) : 0.f;
         if (wave_active && ib >= jb) {
             // Soft-min denominators off the diagonal: Z_ts 2^{-rs} = sv + 2^{PREL_t - rs} with the
             // per-key reference rs = max(C_s, cmid) (sv >= 1 when rs is finite).  With

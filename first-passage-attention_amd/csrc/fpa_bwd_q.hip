@@ -59,7 +59,8 @@ fpa_bwd_q_kernel(BwdParams p) {
     const T *DOb = static_cast<const T *>(p.dout) + b * p.sdo.b + h * p.sdo.h;
     // lanes 0-15: BSUF, 16-31: CP, 32-47: SUFL, 48-63: PHI
     const int kpl = (lane < 16) ? PL_BSUF : (lane < 32) ? PL_CP : (lane < 48) ? PL_SUFL : PL_PHI;
-    const float *kst_src = p.state + L.plane(kpl) + rowbase + 4 * (lane & 15);
+    const float *st_head = p.state + L.at(0, bh, 0);
+    const uint32_t kst_off = (uint32_t)((kpl * p.TP + 4 * (lane & 15)) * 4);  // bytes from plane 0 of the head
 
     TileLoader<T, D, DT, BK, NW> kld, vld;
     kld.init(p.sk.t, w, lane);
@@ -67,7 +68,7 @@ fpa_bwd_q_kernel(BwdParams p) {
     auto issue = [&](int jb, int buf) {
         kld.issue(Ks[buf], Kb, p.sk.t, jb * BK, p.T, w, lane);
         vld.issue(Vs[buf], Vb, p.sv.t, jb * BK, p.T, w, lane);
-        if (w == NW - 1) gl_lds16(kst_src + jb * BK, &kst[buf][0][0]);
+        if (w == NW - 1) buf_lds16(buf_rsrc(st_head + jb * BK), kst_off, &kst[buf][0][0]);
     };
     const int jbmax = min(p.NB - 1, (q0 + BM - 1) / BK);
     issue(jbmax, 0);
@@ -81,9 +82,9 @@ fpa_bwd_q_kernel(BwdParams p) {
     float lse = pinf(), del = 0.f, pre = 0.f, prel = 0.f;
     if (t_valid) {
         lse = p.lse[rowbase + tq];
-        del = p.delta[rowbase + tq];
-        pre = p.state[L.plane(PL_PRE) + rowbase + tq];
-        prel = p.state[L.plane(PL_PREL) + rowbase + tq];
+        del = p.qinfo[qi_at(bh, p.NB, tq, QI_DEL)];
+        pre = p.state[L.at(PL_PRE, bh, tq)];
+        prel = p.state[L.at(PL_PREL, bh, tq)];
     }
     const float ct = -pre * p.il2;  // max a over [start of blk(t), t]
     const float prel_ct = fexp2(prel - ct);
@@ -130,8 +131,8 @@ fpa_bwd_q_kernel(BwdParams p) {
     float racc = 0.f;
     float mid = pinf(), midl = ninf(), cmid = ninf();  // over blocks strictly between jb and ib
     const int ibc = min(ib, p.NB - 1);  // waves past T keep ib in range for these reads
-    const float a_first = -p.state[L.plane(PL_PHI) + rowbase + ibc * G] * p.il2;  // a of the block's first query
-    const float c_blk = -p.state[L.bplane(BP_MIN) + brow + ibc] * p.il2;          // max a over block ib
+    const float a_first = -ld_uniform(p.state, L.at(PL_PHI, bh, ibc * G)) * p.il2;  // a of the block's first query
+    const float c_blk = -ld_uniform(p.state, L.bplane(BP_MIN) + brow + ibc) * p.il2;          // max a over block ib
 
     // BMIN / BLSE of block jb + 1 (which joins the middle), loaded one block ahead.
     float bm_prev = 0.f, bl_prev = 0.f;
@@ -141,9 +142,9 @@ fpa_bwd_q_kernel(BwdParams p) {
         const int buf = it & 1;
         const int s0 = jb * BK;
         if (jb > 0) issue(jb - 1, buf ^ 1);
-        const float bm_here = p.state[L.bplane(BP_MIN) + brow + jb];
-        const float bl_here = p.state[L.bplane(BP_LSE) + brow + jb];
-        const float suf_first = p.state[L.plane(PL_SUF) + rowbase + s0];
+        const float bm_here = ld_uniform(p.state, L.bplane(BP_MIN) + brow + jb);
+        const float bl_here = ld_uniform(p.state, L.bplane(BP_LSE) + brow + jb);
+        const float suf_first = ld_uniform(p.state, L.at(PL_SUF, bh, s0));
         if (wave_active && jb <= ib) {
             const float *kSUF = kst[buf][0], *kPSI = kst[buf][1], *kSUFL = kst[buf][2], *kPHI = kst[buf][3];
             if (jb + 1 < ib) {  // block jb + 1 joins the middle

@@ -342,6 +342,27 @@ __device__ __forceinline__ void gl_lds16(const void *src, void *lds_dst) {
     __builtin_amdgcn_global_load_lds((gbl_void_t *)(src), (lds_void_t *)(lds_dst), 16, 0, 0);
 }
 
+// Raw buffer resource (SGPRs) over bytes [base, base + 2^31) of a wave-uniform pointer.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
+    const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void *>((hi << 32) | lo), (short)0, 0x7fffffff,
+                                             0x00020000);
+}
+
+// 16 bytes per lane from the buffer at byte offset voff straight into LDS at lds_dst + 16 * lane
+// (lds_dst wave-uniform).  Counted by vmcnt like a global load.
+__device__ __forceinline__ void buf_lds16(__amdgpu_buffer_rsrc_t r, uint32_t voff, void *lds_dst) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)(lds_dst), 16, voff, 0, 0, 0);
+}
+
+// Wave-uniform element of memory that the running kernel does not write, read through the scalar
+// cache (counted by lgkmcnt, so it never waits on the vector loads in flight).
+template <typename X> __device__ __forceinline__ X ld_uniform(const X *ptr, int64_t i) {
+    return ((const __attribute__((address_space(4))) X *)ptr)[i];
+}
+
 __device__ __forceinline__ void wait_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // Loads NR-row tiles of one (B, H, T, D)-strided tensor (d stride 1, rows 16-byte aligned,
@@ -369,25 +390,26 @@ template <typename T, int D, int DT, int NR, int NW> struct TileLoader {
             off[j] = (uint32_t)((r * st + lc * P::CE) * (int64_t)sizeof(T));
         }
     }
-    // Rows row0 .. row0 + NR - 1 of the tensor whose row 0 is `base` into `tile`.
+    // Rows row0 .. row0 + NR - 1 (wave-uniform row0 < T_) of the tensor whose row 0 is `base` into
+    // `tile`, through a buffer resource based at row row0 (the offsets stay 32-bit).
     __device__ __forceinline__ void issue(char *tile, const T *base, int64_t st, int row0, int T_, int wave,
                                           int lane) const {
-        const char *b0 = reinterpret_cast<const char *>(base + (int64_t)row0 * st);
+        const __amdgpu_buffer_rsrc_t rs = buf_rsrc(base + (int64_t)row0 * st);
         if (row0 + NR <= T_) {
 #pragma unroll
             for (int j = 0; j < PER; ++j) {
                 const int i = wave + NW * j;
-                if (NI % NW == 0 || i < NI) gl_lds16(b0 + off[j], tile + 1024 * i);
+                if (NI % NW == 0 || i < NI) buf_lds16(rs, off[j], tile + 1024 * i);
             }
         } else {
+            const int rmax = T_ - 1 - row0;  // rows past T read row T - 1
 #pragma unroll
             for (int j = 0; j < PER; ++j) {
                 const int i = wave + NW * j;
                 if (NI % NW == 0 || i < NI) {
                     int r, lc;
                     slot(i, lane, r, lc);
-                    const int row = min(row0 + r, T_ - 1);
-                    gl_lds16(base + (int64_t)row * st + lc * P::CE, tile + 1024 * i);
+                    buf_lds16(rs, (uint32_t)((min(r, rmax) * st + lc * P::CE) * (int64_t)sizeof(T)), tile + 1024 * i);
                 }
             }
         }
@@ -490,6 +512,8 @@ __device__ __forceinline__ void xcd_work_item(int &rank, int &bh, int BH) {
         rank = blockIdx.x;
         bh = blockIdx.y;
     }
+    rank = __builtin_amdgcn_readfirstlane(rank);  // uniform: loop bounds and addresses stay scalar
+    bh = __builtin_amdgcn_readfirstlane(bh);
 }
 
 // Sum over the 64 lanes of a wave, fixed order (butterfly).
@@ -500,11 +524,13 @@ __device__ __forceinline__ float wave_sum(float x) {
 }
 
 
-// State planes (float offsets), each plane is BH * TP floats except the two block planes.
+// State planes (float offsets): NPL per-position planes of TP floats per head, then two block planes.
 constexpr int NPL = 9;  // per-position planes
 struct StateLayout {
     int64_t BH, TP, NB;
-    __host__ __device__ int64_t plane(int k) const { return (int64_t)k * BH * TP; }  // 0 .. NPL-1
+    // Element t of per-position plane k (0 .. NPL-1) of head bh: a head's planes are contiguous
+    // ([bh][k][TP]), so a block's values of several planes sit within 32-bit offsets of each other.
+    __host__ __device__ int64_t at(int k, int64_t bh, int64_t t) const { return (bh * NPL + k) * TP + t; }
     __host__ __device__ int64_t bplane(int k) const { return NPL * BH * TP + (int64_t)k * BH * NB; }  // 0..1
     __host__ __device__ int64_t total() const { return NPL * BH * TP + 2 * BH * NB; }
 };

@@ -67,17 +67,16 @@ __global__ void __launch_bounds__(64) fpa_stats_kernel(StatsParams p) {
         sufl = ninf();
     }
     StateLayout L{p.BH, p.TP, p.NB};
-    const int64_t r = (int64_t)bh * p.TP + u;
-    p.state[L.plane(PL_PHI) + r] = ph;
-    p.state[L.plane(PL_PSI) + r] = ps;
-    p.state[L.plane(PL_PRE) + r] = pm;
-    p.state[L.plane(PL_PREL) + r] = pl;
-    p.state[L.plane(PL_SUF) + r] = suf;
-    p.state[L.plane(PL_SUFL) + r] = sufl;
+    p.state[L.at(PL_PHI, bh, u)] = ph;
+    p.state[L.at(PL_PSI, bh, u)] = ps;
+    p.state[L.at(PL_PRE, bh, u)] = pm;
+    p.state[L.at(PL_PREL, bh, u)] = pl;
+    p.state[L.at(PL_SUF, bh, u)] = suf;
+    p.state[L.at(PL_SUFL, bh, u)] = sufl;
     const float betal = p.beta[bh % p.H] * LOG2E;
-    p.state[L.plane(PL_CA) + r] = betal * fminf(suf - ps, 0.f);
-    p.state[L.plane(PL_CP) + r] = betal * ps;
-    p.state[L.plane(PL_BSUF) + r] = (suf < pinf()) ? betal * suf : (betal > 0.f ? pinf() : betal < 0.f ? ninf() : 0.f);
+    p.state[L.at(PL_CA, bh, u)] = betal * fminf(suf - ps, 0.f);
+    p.state[L.at(PL_CP, bh, u)] = betal * ps;
+    p.state[L.at(PL_BSUF, bh, u)] = (suf < pinf()) ? betal * suf : (betal > 0.f ? pinf() : betal < 0.f ? ninf() : 0.f);
     if (lane == 63) {
         p.state[L.bplane(BP_MIN) + (int64_t)bh * p.NB + blk] = pm;
         p.state[L.bplane(BP_LSE) + (int64_t)bh * p.NB + blk] = pl;
@@ -131,9 +130,10 @@ fpa_fwd_kernel(FwdParams p) {
     const T *Qb = static_cast<const T *>(p.q) + b * p.sq.b + h * p.sq.h;
     const T *Kb = static_cast<const T *>(p.k) + b * p.sk.b + h * p.sk.h;
     const T *Vb = static_cast<const T *>(p.v) + b * p.sv.b + h * p.sv.h;
-    // lanes 0-15: CA, 16-31: CP, 32-63: PHI (the state planes hold TP >= every tile end rows)
-    const float *cst_src = p.state + ((lane < 16) ? L.plane(PL_CA) : (lane < 32) ? L.plane(PL_CP) : L.plane(PL_PHI)) +
-                           rowbase + 4 * (lane & 15);
+    // Per-key values staged with one 64-lane load: lanes 0-15 CA, 16-31 CP, 32-63 PHI (byte offsets
+    // from plane 0 of the head; the state planes hold TP >= every tile end rows).
+    const float *st_head = p.state + L.at(0, bh, 0);
+    const uint32_t cst_off = (uint32_t)((((lane < 16) ? PL_CA : (lane < 32) ? PL_CP : PL_PHI) * p.TP + 4 * (lane & 15)) * 4);
 
     // Tile jt of K, V and the per-key values into buffer `buf` (shared out over the waves).
     TileLoader<T, D, DT, BN, NW> kld, vld;
@@ -142,7 +142,7 @@ fpa_fwd_kernel(FwdParams p) {
     auto issue = [&](int jt, int buf) {
         kld.issue(Ks[buf], Kb, p.sk.t, jt * BN, p.T, w, lane);
         vld.issue(Vs[buf], Vb, p.sv.t, jt * BN, p.T, w, lane);
-        if (w == NW - 1) gl_lds16(cst_src + jt * BN, &cst[buf][0][0]);
+        if (w == NW - 1) buf_lds16(buf_rsrc(st_head + jt * BN), cst_off, &cst[buf][0][0]);
     };
 
     const int nkt = (p.T + BN - 1) / BN;
@@ -154,7 +154,7 @@ fpa_fwd_kernel(FwdParams p) {
 
     const float beta = p.beta[h], betal = beta * LOG2E;
     const float E = (beta >= 0.f) ? ninf() : pinf();
-    const float pre_t = (tq < p.TP) ? p.state[L.plane(PL_PRE) + rowbase + tq] : pinf();
+    const float pre_t = (tq < p.TP) ? p.state[L.at(PL_PRE, bh, tq)] : pinf();
 
     float m_i = ninf(), l_i = 0.f;
     f32x16 oacc[NDT];
@@ -169,7 +169,7 @@ fpa_fwd_kernel(FwdParams p) {
         const int s0 = jt * BN;
         if (jt > 0) issue(jt - 1, buf ^ 1);
         // Issued here, used after the tile: the load's latency hides behind the tile's work.
-        const float bmin_jt = p.state[L.bplane(BP_MIN) + (int64_t)bh * p.NB + jt];
+        const float bmin_jt = ld_uniform(p.state, L.bplane(BP_MIN) + (int64_t)bh * p.NB + jt);
         if (wave_active && s0 <= qw0 + 31) {
             const char *Kt = Ks[buf];
             const float *cA = cst[buf][0], *cP = cst[buf][1], *cPHI = cst[buf][2];

@@ -48,8 +48,7 @@ struct BwdParams {
     float *dpsi;   // (B, H, T) contiguous
     float *dbeta;  // (H,)
     // workspace regions
-    float *qinfo;  // QI_N planes of BH * TP: per-query values of the backward (QI_*)
-    float *delta;  // = qinfo + QI_DEL * BH * TP
+    float *qinfo;  // BH * NB * QI_PLANES * 64: per-query values of the backward (QI_*)
     float *wsum;   // BH * TP   key-block soft-min sums W_s
     float *rsum;   // BH * TP   query-block soft-min sums R_t
     float *gd;     // BH * NB * G * G   gated dS of in-block pairs, [s][t]
@@ -61,9 +60,16 @@ struct BwdParams {
     float il2;     // log2(e) / tau
 };
 
-// Planes of BwdParams::qinfo (each BH * TP floats).  QI_L and QI_D span two planes: row r's
-// pair of 32-bit words sits at 2 r (the key side's folded log-sum-exp and Delta operands).
-enum { QI_L = 0, QI_D = 2, QI_BPRE = 4, QI_ZQ = 5, QI_DEL = 6, QI_N = 7 };
+// BwdParams::qinfo holds, per 64-query block of a head, QI_PLANES planes of 64 floats
+// ([bh][block][plane][64]), so the key side stages a block with two 1 KB loads.  QI_L and QI_D
+// span two planes each: the pair of 32-bit words of row r sits at 2 (r % 64) of that span.
+enum { QI_L = 0, QI_D = 2, QI_BPRE = 4, QI_ZQ = 5, QI_DEL = 6, QI_PLANES = 8 };
+__host__ __device__ inline int64_t qi_at(int64_t bh, int NB, int row, int plane) {
+    return ((bh * NB + row / 64) * QI_PLANES + plane) * 64 + row % 64;
+}
+__host__ __device__ inline int64_t qi_pair_at(int64_t bh, int NB, int row, int plane) {
+    return ((bh * NB + row / 64) * QI_PLANES + plane) * 64 + 2 * (row % 64);
+}
 
 // Launchers (defined next to their kernels); return hipSuccess or the launch error.
 hipError_t launch_stats(const StatsParams &p, hipStream_t s);
