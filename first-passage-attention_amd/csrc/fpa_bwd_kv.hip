@@ -108,6 +108,8 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_prep_kernel(BwdParams p) {
         p.qinfo[qi_at(bh, p.NB, row, QI_BPRE)] = beff * (ok ? p.state[L.at(PL_PRE, bh, row)] : pinf());
         p.qinfo[qi_at(bh, p.NB, row, QI_ZQ)] = (FPA_KV_PROD && spread <= PROD_SPREAD) ? fexp2(prl) : prl;
         p.qinfo[qi_at(bh, p.NB, row, QI_DEL)] = del;
+        // The block's BMIN and BLSE for the key side's loop (plane 7, positions 0 and 1).
+        if (row % G < 2) p.qinfo[qi_at(bh, p.NB, row, QI_BST)] = (row % G == 0) ? p.state[L.bplane(BP_MIN) + (int64_t)bh * p.NB + row / G] : blse;
     }
 }
 
@@ -120,8 +122,7 @@ fpa_bwd_kv_kernel(BwdParams p) {
     constexpr int TB = Pad<T, DT>::template bytes<BQ>();  // one padded Q or dO tile
     __shared__ __attribute__((aligned(1024))) char Qs[2][TB];
     __shared__ __attribute__((aligned(1024))) char dOs[2][TB];
-    // Per-query values of a block: planes 0-1 the L pairs, 2-3 the D pairs, 4 BPRE, 5 ZQ (6-7 copies
-    // of 4-5 that fill the second load instruction).
+    // Per-query values of a block: planes 0-1 the L pairs, 2-3 the D pairs, 4 BPRE, 5 ZQ, 6 DEL, 7 BST.
     __shared__ __attribute__((aligned(1024))) float qi[2][8][BQ];
     __shared__ __attribute__((aligned(16))) float kPHI[BK];
 
@@ -143,8 +144,8 @@ fpa_bwd_kv_kernel(BwdParams p) {
     const T *Kb = static_cast<const T *>(p.k) + b * p.sk.b + h * p.sk.h;
     const T *Vb = static_cast<const T *>(p.v) + b * p.sv.b + h * p.sv.h;
     const T *DOb = static_cast<const T *>(p.dout) + b * p.sdo.b + h * p.sdo.h;
-    // A block's per-query values: planes 0-3 (L and D pairs) and 4-7 (BPRE, ZQ, DEL, spare), one
-    // 1 KB load each.
+    // A block's per-query values: planes 0-3 (L and D pairs) and 4-7 (BPRE, ZQ, DEL, BST), one 1 KB
+    // load each.
     const float *qi_head = p.qinfo + qi_at(bh, p.NB, 0, 0);
 
     TileLoader<T, D, DT, BQ, NW> qld, dld;
@@ -207,14 +208,13 @@ fpa_bwd_kv_kernel(BwdParams p) {
 
     // Block statistics used by a query block, loaded one block ahead: BMIN / BLSE of block
     // ib - 1 (which joins the middle) and BLSE of block ib.
-    float bm_prev = 0.f, bl_prev = 0.f, bl_cur = ld_uniform(p.state, L.bplane(BP_LSE) + brow + ib0);
+    float bm_prev = 0.f, bl_prev = 0.f;  // block ib - 1, from the previous block's staged values
     wait_loads();
     __syncthreads();
     for (int ib = ib0, it = 0; ib < p.NB; ++ib, ++it) {
         const int buf = it & 1;
         if (ib + 1 < p.NB) issue(ib + 1, buf ^ 1);
-        const float bm_here = ld_uniform(p.state, L.bplane(BP_MIN) + brow + ib);
-        const float bl_next = (ib + 1 < p.NB) ? ld_uniform(p.state, L.bplane(BP_LSE) + brow + ib + 1) : 0.f;
+        const float bm_here = qi[buf][QI_BST][0], bl_cur = qi[buf][QI_BST][1];  // block ib
         if (wave_active && ib >= jb) {
             // Soft-min denominators off the diagonal: Z_ts 2^{-rs} = sv + 2^{PREL_t - rs} with the
             // per-key reference rs = max(C_s, cmid) (sv >= 1 when rs is finite).  With
@@ -329,7 +329,6 @@ fpa_bwd_kv_kernel(BwdParams p) {
         }
         bm_prev = bm_here;
         bl_prev = bl_cur;
-        bl_cur = bl_next;
         wait_loads();
         __syncthreads();
     }

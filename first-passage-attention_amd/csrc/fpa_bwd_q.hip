@@ -35,8 +35,9 @@ fpa_bwd_q_kernel(BwdParams p) {
     constexpr int TB = Pad<T, DT>::template bytes<BK>();  // one padded K or V tile
     __shared__ __attribute__((aligned(1024))) char Ks[2][TB];
     __shared__ __attribute__((aligned(1024))) char Vs[2][TB];
-    // Per-key values of a block: BSUF, CP (= betal * psi), SUFL, PHI.
-    __shared__ __attribute__((aligned(1024))) float kst[2][4][BK];
+    // Per-key values of a block: BSUF, CP (= betal * psi), SUFL, PHI, and BST (BMIN, BLSE, SUF of the
+    // first key at [4][0..2]).
+    __shared__ __attribute__((aligned(1024))) float kst[2][5][BK];
     __shared__ __attribute__((aligned(16))) float Aw[NW][BK];  // per-wave key factors of the shared-reference path
 
     const int tid = threadIdx.x, lane = tid % 64, g = lane / 32, c = lane % 32;
@@ -61,6 +62,7 @@ fpa_bwd_q_kernel(BwdParams p) {
     const int kpl = (lane < 16) ? PL_BSUF : (lane < 32) ? PL_CP : (lane < 48) ? PL_SUFL : PL_PHI;
     const float *st_head = p.state + L.at(0, bh, 0);
     const uint32_t kst_off = (uint32_t)((kpl * p.TP + 4 * (lane & 15)) * 4);  // bytes from plane 0 of the head
+    const uint32_t bst_off = (uint32_t)((PL_BST * p.TP + lane) * 4);
 
     TileLoader<T, D, DT, BK, NW> kld, vld;
     kld.init(p.sk.t, w, lane);
@@ -69,8 +71,9 @@ fpa_bwd_q_kernel(BwdParams p) {
         kld.issue(Ks[buf], Kb, p.sk.t, jb * BK, p.T, w, lane);
         vld.issue(Vs[buf], Vb, p.sv.t, jb * BK, p.T, w, lane);
         if (w == NW - 1) buf_lds16(buf_rsrc(st_head + jb * BK), kst_off, &kst[buf][0][0]);
+        if (w == (NW >= 2 ? NW - 2 : 0)) buf_lds4(buf_rsrc(st_head + jb * BK), bst_off, &kst[buf][4][0]);
     };
-    const int jbmax = min(p.NB - 1, (q0 + BM - 1) / BK);
+    const int jbmax = umin_i(p.NB - 1, (q0 + BM - 1) / BK);
     issue(jbmax, 0);
 
     OpRow<T, D> qreg, doreg;
@@ -130,11 +133,11 @@ fpa_bwd_q_kernel(BwdParams p) {
     for (int dt = 0; dt < NDT; ++dt) dqacc[dt] = zero16();
     float racc = 0.f;
     float mid = pinf(), midl = ninf(), cmid = ninf();  // over blocks strictly between jb and ib
-    const int ibc = min(ib, p.NB - 1);  // waves past T keep ib in range for these reads
+    const int ibc = umin_i(ib, p.NB - 1);  // waves past T keep ib in range for these reads
     const float a_first = -ld_uniform(p.state, L.at(PL_PHI, bh, ibc * G)) * p.il2;  // a of the block's first query
     const float c_blk = -ld_uniform(p.state, L.bplane(BP_MIN) + brow + ibc) * p.il2;          // max a over block ib
 
-    // BMIN / BLSE of block jb + 1 (which joins the middle), loaded one block ahead.
+    // BMIN / BLSE of block jb + 1 (which joins the middle), from the previous block's staged values.
     float bm_prev = 0.f, bl_prev = 0.f;
     wait_loads();
     __syncthreads();
@@ -142,9 +145,7 @@ fpa_bwd_q_kernel(BwdParams p) {
         const int buf = it & 1;
         const int s0 = jb * BK;
         if (jb > 0) issue(jb - 1, buf ^ 1);
-        const float bm_here = ld_uniform(p.state, L.bplane(BP_MIN) + brow + jb);
-        const float bl_here = ld_uniform(p.state, L.bplane(BP_LSE) + brow + jb);
-        const float suf_first = ld_uniform(p.state, L.at(PL_SUF, bh, s0));
+        const float bm_here = kst[buf][4][0], bl_here = kst[buf][4][1], suf_first = kst[buf][4][2];
         if (wave_active && jb <= ib) {
             const float *kSUF = kst[buf][0], *kPSI = kst[buf][1], *kSUFL = kst[buf][2], *kPHI = kst[buf][3];
             if (jb + 1 < ib) {  // block jb + 1 joins the middle

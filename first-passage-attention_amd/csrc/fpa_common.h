@@ -66,6 +66,9 @@ __device__ __forceinline__ float lse2_pair(float a, float b) {
 // Element (row, column) of accumulator register j for lane group g (column = lane % 32).
 __device__ __forceinline__ constexpr int acc_row(int j, int g) { return 8 * (j / 4) + 4 * g + (j % 4); }
 
+// Minimum of two wave-uniform ints, kept in SGPRs (loop bounds stay scalar).
+__device__ __forceinline__ int umin_i(int a, int b) { return __builtin_amdgcn_readfirstlane(a < b ? a : b); }
+
 __device__ __forceinline__ float uniform_f(float x) {  // value of the first active lane
     return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x)));
 }
@@ -357,6 +360,11 @@ __device__ __forceinline__ void buf_lds16(__amdgpu_buffer_rsrc_t r, uint32_t vof
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)(lds_dst), 16, voff, 0, 0, 0);
 }
 
+// 4 bytes per lane (lds_dst + 4 * lane).
+__device__ __forceinline__ void buf_lds4(__amdgpu_buffer_rsrc_t r, uint32_t voff, void *lds_dst) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)(lds_dst), 4, voff, 0, 0, 0);
+}
+
 // Wave-uniform element of memory that the running kernel does not write, read through the scalar
 // cache (counted by lgkmcnt, so it never waits on the vector loads in flight).
 template <typename X> __device__ __forceinline__ X ld_uniform(const X *ptr, int64_t i) {
@@ -525,7 +533,7 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 
 // State planes (float offsets): NPL per-position planes of TP floats per head, then two block planes.
-constexpr int NPL = 9;  // per-position planes
+constexpr int NPL = 10;  // per-position planes
 struct StateLayout {
     int64_t BH, TP, NB;
     // Element t of per-position plane k (0 .. NPL-1) of head bh: a head's planes are contiguous
@@ -536,7 +544,11 @@ struct StateLayout {
 };
 // Per-key bias terms, betal = beta * log2(e): PL_CA = betal * min(SUF - psi, 0), PL_CP = betal * psi,
 // PL_BSUF = betal * SUF (an infinite SUF keeps the sign of beta, and gives 0 when beta = 0).
-enum { PL_PHI = 0, PL_PSI = 1, PL_PRE = 2, PL_PREL = 3, PL_SUF = 4, PL_SUFL = 5, PL_CA = 6, PL_CP = 7, PL_BSUF = 8 };
+// PL_BST holds, at positions 0, 1, 2 of each block, the block's BMIN, BLSE and SUF of its first
+// position (0 elsewhere): staged with a tile, the kernels read them from LDS, never from memory
+// inside their loops.
+enum { PL_PHI = 0, PL_PSI = 1, PL_PRE = 2, PL_PREL = 3, PL_SUF = 4, PL_SUFL = 5, PL_CA = 6, PL_CP = 7, PL_BSUF = 8,
+       PL_BST = 9 };
 enum { BP_MIN = 0, BP_LSE = 1 };
 
 }  // namespace fpa

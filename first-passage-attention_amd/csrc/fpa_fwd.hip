@@ -77,6 +77,8 @@ __global__ void __launch_bounds__(64) fpa_stats_kernel(StatsParams p) {
     p.state[L.at(PL_CA, bh, u)] = betal * fminf(suf - ps, 0.f);
     p.state[L.at(PL_CP, bh, u)] = betal * ps;
     p.state[L.at(PL_BSUF, bh, u)] = (suf < pinf()) ? betal * suf : (betal > 0.f ? pinf() : betal < 0.f ? ninf() : 0.f);
+    const float bmin = __shfl(pm, 63, 64), blse = __shfl(pl, 63, 64), suf0 = __shfl(suf, 0, 64);
+    p.state[L.at(PL_BST, bh, u)] = (lane == 0) ? bmin : (lane == 1) ? blse : (lane == 2) ? suf0 : 0.f;
     if (lane == 63) {
         p.state[L.bplane(BP_MIN) + (int64_t)bh * p.NB + blk] = pm;
         p.state[L.bplane(BP_LSE) + (int64_t)bh * p.NB + blk] = pl;
@@ -112,7 +114,7 @@ fpa_fwd_kernel(FwdParams p) {
     constexpr int TB = Pad<T, DT>::template bytes<BN>();  // one padded K or V tile
     __shared__ __attribute__((aligned(1024))) char Ks[2][TB];
     __shared__ __attribute__((aligned(1024))) char Vs[2][TB];
-    // Per-key values of a tile: CA, CP, PHI (and a copy of PHI that fills the load instruction).
+    // Per-key values of a tile: CA, CP, PHI and BST (the block's BMIN at [3][0]).
     __shared__ __attribute__((aligned(1024))) float cst[2][4][BN];
 
     const int tid = threadIdx.x, lane = tid % 64, g = lane / 32, c = lane % 32;
@@ -130,10 +132,10 @@ fpa_fwd_kernel(FwdParams p) {
     const T *Qb = static_cast<const T *>(p.q) + b * p.sq.b + h * p.sq.h;
     const T *Kb = static_cast<const T *>(p.k) + b * p.sk.b + h * p.sk.h;
     const T *Vb = static_cast<const T *>(p.v) + b * p.sv.b + h * p.sv.h;
-    // Per-key values staged with one 64-lane load: lanes 0-15 CA, 16-31 CP, 32-63 PHI (byte offsets
-    // from plane 0 of the head; the state planes hold TP >= every tile end rows).
+    // Per-key values staged with one 64-lane load: lanes 0-15 CA, 16-31 CP, 32-47 PHI, 48-63 BST (byte
+    // offsets from plane 0 of the head; the state planes hold TP >= every tile end rows).
     const float *st_head = p.state + L.at(0, bh, 0);
-    const uint32_t cst_off = (uint32_t)((((lane < 16) ? PL_CA : (lane < 32) ? PL_CP : PL_PHI) * p.TP + 4 * (lane & 15)) * 4);
+    const uint32_t cst_off = (uint32_t)((((lane < 16) ? PL_CA : (lane < 32) ? PL_CP : (lane < 48) ? PL_PHI : PL_BST) * p.TP + 4 * (lane & 15)) * 4);
 
     // Tile jt of K, V and the per-key values into buffer `buf` (shared out over the waves).
     TileLoader<T, D, DT, BN, NW> kld, vld;
@@ -146,7 +148,7 @@ fpa_fwd_kernel(FwdParams p) {
     };
 
     const int nkt = (p.T + BN - 1) / BN;
-    const int jtmax = min(nkt - 1, (q0 + BM - 1) / BN);
+    const int jtmax = umin_i(nkt - 1, (q0 + BM - 1) / BN);
     issue(jtmax, 0);
 
     OpRow<T, D> qreg;
@@ -168,8 +170,6 @@ fpa_fwd_kernel(FwdParams p) {
         const int buf = it & 1;
         const int s0 = jt * BN;
         if (jt > 0) issue(jt - 1, buf ^ 1);
-        // Issued here, used after the tile: the load's latency hides behind the tile's work.
-        const float bmin_jt = ld_uniform(p.state, L.bplane(BP_MIN) + (int64_t)bh * p.NB + jt);
         if (wave_active && s0 <= qw0 + 31) {
             const char *Kt = Ks[buf];
             const float *cA = cst[buf][0], *cP = cst[buf][1], *cPHI = cst[buf][2];
@@ -267,7 +267,7 @@ fpa_fwd_kernel(FwdParams p) {
                 }
             }
 
-            if (jb < ib) mid = fminf(mid, bmin_jt);
+            if (jb < ib) mid = fminf(mid, cst[buf][3][0]);  // BMIN of block jb
         }
         wait_loads();
         __syncthreads();

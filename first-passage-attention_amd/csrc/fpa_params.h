@@ -63,7 +63,8 @@ struct BwdParams {
 // BwdParams::qinfo holds, per 64-query block of a head, QI_PLANES planes of 64 floats
 // ([bh][block][plane][64]), so the key side stages a block with two 1 KB loads.  QI_L and QI_D
 // span two planes each: the pair of 32-bit words of row r sits at 2 (r % 64) of that span.
-enum { QI_L = 0, QI_D = 2, QI_BPRE = 4, QI_ZQ = 5, QI_DEL = 6, QI_PLANES = 8 };
+// QI_BST holds the block's BMIN and BLSE at positions 0 and 1.
+enum { QI_L = 0, QI_D = 2, QI_BPRE = 4, QI_ZQ = 5, QI_DEL = 6, QI_BST = 7, QI_PLANES = 8 };
 __host__ __device__ inline int64_t qi_at(int64_t bh, int NB, int row, int plane) {
     return ((bh * NB + row / 64) * QI_PLANES + plane) * 64 + row % 64;
 }
