@@ -2,6 +2,7 @@
 """Benchmark of First Passage Attention on one MI355X (the BASELINE.json metric).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4]
+    python bench.py --workload lm [--steps K] [--warmup W]     # cfg5 LM training step
 
 A step is one forward + backward of ``first_passage_attention(..., impl="hip")`` over
 one batch of synthetic inputs already resident in HBM (BASELINE.json config 2 by
@@ -10,6 +11,11 @@ beta = 1; gradients of o.float().sum() w.r.t. q, k, v, phi, psi, beta).  W untim
 steps, then K steps timed between two device synchronisations.  Rank 0 prints one
 JSON line.  ``value`` is fwd+bwd TFLOP/s of the algorithmic flops 14*D*P
 (P = B*H*T*(T+1)/2 causal pairs; bias and soft-min work not counted).
+
+``--workload lm`` times instead one training step (fp16 autocast forward, backward with a
+gradient scaler, AdamW update) of fpa.lm.FPADecoder, a 12-layer d768 H12 pre-norm decoder
+whose attention is the FirstPassageAttention layer on the HIP kernels, over B8 x T2048 random
+tokens (cfg5); ``value`` is tokens per second.
 
 Per-kernel times come from HIP events recorded on torch's current stream (the stream
 every kernel is launched on) around C-ABI calls that enqueue one kernel each; the
@@ -98,12 +104,71 @@ def cpu_baseline(cfg, seconds):
                       f"median {t:.3f} s/head"}
 
 
+LM = dict(B=8, T=2048, d_model=768, n_heads=12, layers=12, d_mlp=3072, vocab=32000)
+
+
+def run_lm(a):
+    """cfg5: tokens/s of one LM training step (see the module docstring)."""
+    import torch
+    from fpa.lm import FPADecoder
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    torch.manual_seed(0)
+    model = FPADecoder(LM["vocab"], LM["d_model"], LM["n_heads"], LM["layers"], LM["d_mlp"], impl="hip").to(dev)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4)
+    scaler = torch.amp.GradScaler("cuda")
+    g = torch.Generator().manual_seed(0)
+    tokens = torch.randint(0, LM["vocab"], (LM["B"], LM["T"] + 1), generator=g).to(dev)
+
+    def step():
+        with torch.autocast("cuda", dtype=torch.float16):
+            loss = model.loss(tokens)
+        opt.zero_grad(set_to_none=True)
+        scaler.scale(loss).backward()
+        scaler.step(opt)
+        scaler.update()
+        return loss
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        loss = step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / a.steps
+    ntok = LM["B"] * LM["T"]
+    res = {
+        "metric": "LM training step tokens/s (cfg5: 12-layer d768 H12 FPA decoder, B8 T2048, fp16 autocast)",
+        "value": round(ntok / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (uniform random tokens, random-init weights)",
+        "config": {"workload": "cfg5: FPADecoder training step (AdamW, grad scaler)", **LM,
+                   "parallelism": "single GPU"},
+        "final_loss": round(loss.item(), 4),
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(res), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
+    ap.add_argument("--workload", default="fpa", choices=("fpa", "lm"),
+                    help="fpa: the attention forward+backward of --config; lm: the cfg5 LM training step")
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
@@ -115,6 +180,10 @@ def main():
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(FPA shards over batch and heads with no communication; see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
+
+    if a.workload == "lm":
+        run_lm(a)
+        return
 
     import torch
     import fpa
