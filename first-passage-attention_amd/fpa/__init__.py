@@ -25,19 +25,8 @@ def _pow2(n):
     return n >= 16 and n & (n - 1) == 0
 
 
-def first_passage_attention(q, k, v, phi, psi, beta, tau=1.0, impl=None, block=64):
-    """o (B, H, T, D) of q, k, v (B, H, T, D), phi, psi (B, H, T) and beta (H,).
-
-    impl: "hip" (q, k, v all fp16 or all fp32; D a power of two >= 16), "reference"
-    (any device), or None for "hip" on GPU tensors and "reference" otherwise.
-    block: validated like the reference's (a power of two >= 16); the HIP kernels
-    choose their own tiles, so it does not change the result.
-    Validation order and messages follow kernel.py:463-486.
-    """
-    if impl is None:
-        impl = "hip" if q.is_cuda else "reference"
-    if impl == "reference":
-        return dense.causal_attention(q, k, v, first_passage_bias(phi, psi, beta, tau))
+def _check_hip(q, k, v, phi, psi, beta, tau, impl, block):
+    """The reference's validation (kernel.py:463-486, same order and messages); returns beta as (H,)."""
     if impl not in _HIP_NAMES:
         raise ValueError(f"unknown implementation {impl!r}")
     if q.dim() != 4 or k.shape != q.shape or v.shape != q.shape:
@@ -60,8 +49,41 @@ def first_passage_attention(q, k, v, phi, psi, beta, tau=1.0, impl=None, block=6
         raise ValueError("tau must be positive")
     if not q.is_cuda:
         raise RuntimeError("impl='hip' needs q, k, v on a ROCm GPU")
+    return beta
+
+
+def first_passage_attention(q, k, v, phi, psi, beta, tau=1.0, impl=None, block=64):
+    """o (B, H, T, D) of q, k, v (B, H, T, D), phi, psi (B, H, T) and beta (H,).
+
+    impl: "hip" (q, k, v all fp16 or all fp32; D a power of two >= 16), "reference"
+    (any device), or None for "hip" on GPU tensors and "reference" otherwise.
+    block: validated like the reference's (a power of two >= 16); the HIP kernels
+    choose their own tiles, so it does not change the result.
+    Validation order and messages follow kernel.py:463-486.
+    """
+    if impl is None:
+        impl = "hip" if q.is_cuda else "reference"
+    if impl == "reference":
+        return dense.causal_attention(q, k, v, first_passage_bias(phi, psi, beta, tau))
+    beta = _check_hip(q, k, v, phi, psi, beta, tau, impl, block)
     from ._hip import FirstPassageAttentionHIP  # loads libfpa.so; raises if it is missing
     return FirstPassageAttentionHIP.apply(q, k, v, phi.float(), psi.float(), beta.float(), tau)
+
+
+def _attention_packed(qkv, phi, psi, beta, tau, impl, block):
+    """The layer's attention on its projection output qkv (B, T, 3, H, D): o as (B, T, H, D).
+
+    On the HIP kernels q, k, v are read as strided views of qkv, o is written in (B, T, H, D)
+    order and the backward writes d(qkv) in qkv's own layout, so the layer copies nothing
+    around the attention (the reference pads and copies, kernel.py:380-384, 527)."""
+    q, k, v = qkv.permute(2, 0, 3, 1, 4)
+    if impl is None:
+        impl = "hip" if qkv.is_cuda else "reference"
+    if impl == "reference":
+        return first_passage_attention(q, k, v, phi, psi, beta, tau, impl, block).transpose(1, 2)
+    beta = _check_hip(q, k, v, phi, psi, beta, tau, impl, block)
+    from ._hip import FirstPassageAttentionPackedHIP
+    return FirstPassageAttentionPackedHIP.apply(qkv, phi.float(), psi.float(), beta.float(), tau)
 
 
 class Field(nn.Module):
@@ -101,7 +123,7 @@ class FirstPassageAttention(nn.Module):
 
     def forward(self, x):
         B, T, _ = x.shape
-        q, k, v = self.qkv(x).view(B, T, 3, self.h, self.d).permute(2, 0, 3, 1, 4)
+        qkv = self.qkv(x).view(B, T, 3, self.h, self.d)
         phi, psi, beta = self.field(x)
-        o = first_passage_attention(q, k, v, phi, psi, beta, tau=self.tau, impl=self.impl, block=self.block)
-        return self.out(o.transpose(1, 2).reshape(B, T, -1))
+        o = _attention_packed(qkv, phi, psi, beta, self.tau, self.impl, self.block)  # (B, T, H, D)
+        return self.out(o.reshape(B, T, -1))

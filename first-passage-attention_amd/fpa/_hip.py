@@ -29,11 +29,11 @@ def rows(t):
 class FwdBuffers:
     """Outputs and saved state of one forward call (all allocated by torch on q's device)."""
 
-    def __init__(self, q):
+    def __init__(self, q, o=None):
         L = _lib.lib()
         B, H, T, D = q.shape
         dev = q.device
-        self.o = torch.empty((B, H, T, D), dtype=q.dtype, device=dev)
+        self.o = torch.empty((B, H, T, D), dtype=q.dtype, device=dev) if o is None else o
         self.lse = torch.empty(L.fpa_lse_floats(B, H, T), dtype=torch.float32, device=dev)
         self.state = torch.empty(L.fpa_state_floats(B, H, T), dtype=torch.float32, device=dev)
 
@@ -41,13 +41,16 @@ class FwdBuffers:
 class BwdBuffers:
     """Gradients and scratch of one backward call."""
 
-    def __init__(self, q):
+    def __init__(self, q, dqkv=None):
         L = _lib.lib()
         B, H, T, D = q.shape
         dev = q.device
-        self.dq = torch.empty((B, H, T, D), dtype=q.dtype, device=dev)
-        self.dk = torch.empty_like(self.dq)
-        self.dv = torch.empty_like(self.dq)
+        if dqkv is None:
+            self.dq = torch.empty((B, H, T, D), dtype=q.dtype, device=dev)
+            self.dk = torch.empty_like(self.dq)
+            self.dv = torch.empty_like(self.dq)
+        else:  # strided views of one (B, T, 3, H, D) buffer
+            self.dq, self.dk, self.dv = dqkv.permute(2, 0, 3, 1, 4)
         self.dphi = torch.empty((B, H, T), dtype=torch.float32, device=dev)
         self.dpsi = torch.empty_like(self.dphi)
         self.dbeta = torch.empty(H, dtype=torch.float32, device=dev)
@@ -134,3 +137,35 @@ class FirstPassageAttentionHIP(torch.autograd.Function):
             grads = BwdBuffers(q)
             run_bwd(bwd_args(q, k, v, beta, ctx.tau, _Saved(o, lse, state), do, grads), dev)
         return grads.dq, grads.dk, grads.dv, grads.dphi, grads.dpsi, grads.dbeta, None
+
+
+class FirstPassageAttentionPackedHIP(torch.autograd.Function):
+    """The layer's path: qkv (B, T, 3, H, D) -> o (B, T, H, D); the backward returns d(qkv) in
+    qkv's layout.  The kernels read and write every tensor through its strides, so there is no
+    copy on either side of the attention."""
+
+    @staticmethod
+    def forward(ctx, qkv, phi, psi, beta, tau):
+        B, T, _, H, D = qkv.shape
+        q, k, v = (rows(t) for t in qkv.permute(2, 0, 3, 1, 4))
+        beta = beta.contiguous()
+        dev = qkv.device
+        with torch.cuda.device(dev):
+            o_bthd = torch.empty((B, T, H, D), dtype=qkv.dtype, device=dev)
+            out = FwdBuffers(q, o=o_bthd.permute(0, 2, 1, 3))
+            run_fwd(fwd_args(q, k, v, phi, psi, beta, tau, out), dev)
+        ctx.save_for_backward(q, k, v, out.o, out.lse, out.state, beta)
+        ctx.tau = float(tau)
+        return o_bthd
+
+    @staticmethod
+    def backward(ctx, do_bthd):
+        q, k, v, o, lse, state, beta = ctx.saved_tensors
+        B, H, T, D = q.shape
+        dev = q.device
+        do = rows(do_bthd.to(q.dtype).permute(0, 2, 1, 3))
+        with torch.cuda.device(dev):
+            dqkv = torch.empty((B, T, 3, H, D), dtype=q.dtype, device=dev)
+            grads = BwdBuffers(q, dqkv=dqkv)
+            run_bwd(bwd_args(q, k, v, beta, ctx.tau, _Saved(o, lse, state), do, grads), dev)
+        return dqkv, grads.dphi, grads.dpsi, grads.dbeta, None
