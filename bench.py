@@ -214,6 +214,27 @@ def main():
     torch.cuda.synchronize()
     fwd_bwd_ms = (time.perf_counter() - t0) * 1e3 / a.steps
 
+    # The same step captured once in a HIP graph and replayed: the kernels without the host's
+    # launch gaps (reported beside the eager step, which stays the bench value).
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(a.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    graph_ms = (time.perf_counter() - t0) * 1e3 / a.steps
+    del graph
+
     with torch.no_grad():
         for _ in range(a.warmup):
             fpa.first_passage_attention(q, k, v, phi, psi, beta, impl="hip")
@@ -288,6 +309,7 @@ def main():
                    "B": cfg["B"], "H": cfg["H"], "T": cfg["T"], "D": D, "parallelism": "single GPU"},
         "fwd_ms": round(fwd_ms, 4),
         "fwd_bwd_ms": round(fwd_bwd_ms, 4),
+        "fwd_bwd_graph_ms": round(graph_ms, 4),
         "fwd_tflops": round(fwd_tflops, 3),
         "fwd_pct_peak": round(100 * fwd_tflops / peak, 2),
         "fwd_bwd_pct_peak": round(100 * fb_tflops / peak, 2),
