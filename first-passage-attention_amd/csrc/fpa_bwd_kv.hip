@@ -29,29 +29,16 @@
 namespace fpa {
 
 // Per-query planes of the backward (QI_*), for t < TP:
-//   L, D  the key side's extra contraction step that subtracts lse_t / sc2 from S and Delta_t from
-//         dP on the MFMA: with the key-side operand {2048, 1, 1} (fp16) the query-side operand is
-//         {-a, -b, -c}, a = fp16(rint(x / 2048)), b = fp16(x - 2048 a), c = fp16(x - 2048 a - b)
-//         (x = lse_t / sc2 resp. Delta_t; |x| < 1.3e8); fp32 keys take {1} and {-x}.  Rows past T
-//         get a = 65504 (fp16) or x = 1e30 (fp32): their scores become hugely negative and P = 0
-//         there with no per-element mask.  Delta_t = sum_d dO_td O_td (0 past T).
+//   LQ    -lse_t / sc2 (-inf past T) and DL = -Delta_t (0 past T), Delta_t = sum_d dO_td O_td: the
+//         start values of the S and dP accumulators, so the MFMA chains subtract them for free;
+//         rows past T get -inf scores and P = 0 with no per-element mask
 //   BPRE  beff * PRE_t (beff = beta * log2e, or 2^-100 for beta = 0; +-inf past T)
 //   ZQ    with PRL_t = PREL_t - BLSE <= 0 (BLSE = log2 sum 2^a over t's block; 0 past T):
 //         2^{PRL_t} > 0 when the block's spread -PRL_{first row} is at most PROD_SPREAD
 //         (product form of the soft-min denominators), else PRL_t <= 0 (exact form).  The sign
 //         of the block's first entry tells the two apart.
-//   DEL   Delta_t in fp32 (the query side's operand).
+//   BST   the block's BMIN and BLSE (positions 0 and 1).
 __device__ __forceinline__ float beta_eff(float betal) { return betal != 0.f ? betal : 0x1p-100f; }
-
-// Three fp16 terms x = 2048 a + b + c (see QI_L), negated and packed as two 32-bit words.
-__device__ __forceinline__ void fold_terms(float x, float &w0, float &w1) {
-    const f16 a = (f16)fminf(fmaxf(rintf(x * (1.f / 2048.f)), -65504.f), 65504.f);
-    const float r = x - 2048.f * (float)a;
-    const f16 bb = (f16)r, cc = (f16)(r - (float)bb);
-    const h2 v0 = {(f16)-a, (f16)-bb}, v1 = {(f16)-cc, (f16)0.f};
-    w0 = __builtin_bit_cast(float, v0);
-    w1 = __builtin_bit_cast(float, v1);
-}
 
 template <typename T, int D>
 __global__ void __launch_bounds__(NTHREADS) fpa_bwd_prep_kernel(BwdParams p) {
@@ -87,27 +74,10 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_prep_kernel(BwdParams p) {
         const float prl = ok ? p.state[L.at(PL_PREL, bh, row)] - blse : 0.f;
         const float spread = blse - p.state[L.at(PL_PREL, bh, (row / G) * G)];
         const float beff = beta_eff(p.beta[bh % p.H] * LOG2E);
-        const float del = ok ? acc : 0.f;
-        float l0, l1, d0, d1;
-        if constexpr (sizeof(T) == 2) {
-            if (ok) {
-                fold_terms(p.lse[r] / p.sc2, l0, l1);
-            } else {
-                const h2 big = {(f16)-65504.f, (f16)0.f};
-                l0 = __builtin_bit_cast(float, big);
-                l1 = 0.f;
-            }
-            fold_terms(del, d0, d1);
-        } else {
-            l0 = ok ? -p.lse[r] / p.sc2 : -1e30f;
-            d0 = -del;
-            l1 = d1 = 0.f;
-        }
-        *reinterpret_cast<f32x2 *>(&p.qinfo[qi_pair_at(bh, p.NB, row, QI_L)]) = f32x2{l0, l1};
-        *reinterpret_cast<f32x2 *>(&p.qinfo[qi_pair_at(bh, p.NB, row, QI_D)]) = f32x2{d0, d1};
+        p.qinfo[qi_at(bh, p.NB, row, QI_LQ)] = ok ? -p.lse[r] / p.sc2 : ninf();
+        p.qinfo[qi_at(bh, p.NB, row, QI_DL)] = ok ? -acc : 0.f;
         p.qinfo[qi_at(bh, p.NB, row, QI_BPRE)] = beff * (ok ? p.state[L.at(PL_PRE, bh, row)] : pinf());
         p.qinfo[qi_at(bh, p.NB, row, QI_ZQ)] = (FPA_KV_PROD && spread <= PROD_SPREAD) ? fexp2(prl) : prl;
-        p.qinfo[qi_at(bh, p.NB, row, QI_DEL)] = del;
         // The block's BMIN and BLSE for the key side's loop (plane 7, positions 0 and 1).
         if (row % G < 2) p.qinfo[qi_at(bh, p.NB, row, QI_BST)] = (row % G == 0) ? p.state[L.bplane(BP_MIN) + (int64_t)bh * p.NB + row / G] : blse;
     }
@@ -122,8 +92,8 @@ fpa_bwd_kv_kernel(BwdParams p) {
     constexpr int TB = Pad<T, DT>::template bytes<BQ>();  // one padded Q or dO tile
     __shared__ __attribute__((aligned(1024))) char Qs[2][TB];
     __shared__ __attribute__((aligned(1024))) char dOs[2][TB];
-    // Per-query values of a block: planes 0-1 the L pairs, 2-3 the D pairs, 4 BPRE, 5 ZQ, 6 DEL, 7 BST.
-    __shared__ __attribute__((aligned(1024))) float qi[2][8][BQ];
+    // Per-query values of a block: LQ, DL, BPRE, ZQ, BST.
+    __shared__ __attribute__((aligned(1024))) float qi[2][5][BQ];
     __shared__ __attribute__((aligned(16))) float kPHI[BK];
 
     const int tid = threadIdx.x, lane = tid % 64, g = lane / 32, c = lane % 32;
@@ -144,8 +114,7 @@ fpa_bwd_kv_kernel(BwdParams p) {
     const T *Kb = static_cast<const T *>(p.k) + b * p.sk.b + h * p.sk.h;
     const T *Vb = static_cast<const T *>(p.v) + b * p.sv.b + h * p.sv.h;
     const T *DOb = static_cast<const T *>(p.dout) + b * p.sdo.b + h * p.sdo.h;
-    // A block's per-query values: planes 0-3 (L and D pairs) and 4-7 (BPRE, ZQ, DEL, BST), one 1 KB
-    // load each.
+    // A block's per-query values: planes 0-3 (LQ, DL, BPRE, ZQ) with one 1 KB load, BST with a 256 B one.
     const float *qi_head = p.qinfo + qi_at(bh, p.NB, 0, 0);
 
     TileLoader<T, D, DT, BQ, NW> qld, dld;
@@ -156,7 +125,7 @@ fpa_bwd_kv_kernel(BwdParams p) {
         dld.issue(dOs[buf], DOb, p.sdo.t, ib * BQ, p.T, w, lane);
         if (w == NW - 1) buf_lds16(buf_rsrc(qi_head + (int64_t)ib * QI_PLANES * 64), 16 * lane, &qi[buf][0][0]);
         if (w == (NW >= 2 ? NW - 2 : 0))
-            buf_lds16(buf_rsrc(qi_head + (int64_t)ib * QI_PLANES * 64), 1024 + 16 * lane, &qi[buf][4][0]);
+            buf_lds4(buf_rsrc(qi_head + (int64_t)ib * QI_PLANES * 64), 4 * (QI_BST * 64 + lane), &qi[buf][4][0]);
     };
     const int ib0 = k0 / G;
     issue(ib0, 0);
@@ -178,21 +147,17 @@ fpa_bwd_kv_kernel(BwdParams p) {
     }
     const float Cs = (suf < pinf()) ? -suf * p.il2 : ninf();  // max a over (s, end of block)
     const float bsuf = beff * suf, bpsi = beff * psi_s;
-    // The key side's operand of the extra contraction step (see QI_L): {2048, 1, 1} / {1}.
-    typename MT<T>::op_t kone;
-    if constexpr (sizeof(T) == 2) {
-        const f16 z = (f16)0.f, o = (f16)1.f;
-        kone = g ? h8{z, z, z, z, z, z, z, z} : h8{(f16)2048.f, o, o, z, z, z, z, z};
-    } else {
-        kone = g ? 0.f : 1.f;
-    }
-    // Query-side operand of row `row` from a pair plane of the staged block.
-    auto aug_op = [&](const float *pairs, int row) {
-        const f32x2 v = *reinterpret_cast<const f32x2 *>(&pairs[2 * row]);
-        if constexpr (sizeof(T) == 2)
-            return __builtin_bit_cast(h8, f32x4{v[0], v[1], 0.f, 0.f});
-        else
-            return v[0];
+    // Accumulator start values from a per-query plane of the staged block: register j of this
+    // lane holds row 32 mt + 8 (j / 4) + 4 g + j % 4.
+    auto rows16 = [&](const float *plane, int mt) {
+        f32x16 r;
+#pragma unroll
+        for (int jq = 0; jq < 4; ++jq) {
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(&plane[32 * mt + 8 * jq + 4 * g]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) r[4 * jq + e] = v[e];
+        }
+        return r;
     };
     if (tid < BK) kPHI[tid] = (k0 + tid < p.TP) ? p.state[L.at(PL_PHI, bh, k0 + tid)] : pinf();
 
@@ -240,7 +205,7 @@ fpa_bwd_kv_kernel(BwdParams p) {
             const float cA = __builtin_amdgcn_fmed3f(bsuf, beff * mid, E);  // beff * min(SUF_s, MID)
             const char *Qt = Qs[buf];
             const char *Dt = dOs[buf];
-            const float *rBPRE = qi[buf][4];
+            const float *rBPRE = qi[buf][QI_BPRE];
             const bool diag = (ib == jb);
             const int sr = s - sb;
             float r = pinf();  // running min of phi over (s, u] for the in-block scan
@@ -249,10 +214,8 @@ fpa_bwd_kv_kernel(BwdParams p) {
             for (int mt = 0; mt < 2; ++mt) {
                 f32x16 S, dP;
                 // S - lse / sc2 and dP - Delta, rows t, columns s
-                S = MT<T>::mma(aug_op(qi[buf][0], 32 * mt + c), kone,
-                               mma_p1_pad_reg<T, D, DT>(zero16(), Qt, 32 * mt + c, g, kreg));
-                dP = MT<T>::mma(aug_op(qi[buf][2], 32 * mt + c), kone,
-                                mma_p1_pad_reg<T, D, DT>(zero16(), Dt, 32 * mt + c, g, vreg));
+                S = mma_p1_pad_reg<T, D, DT>(rows16(qi[buf][QI_LQ], mt), Qt, 32 * mt + c, g, kreg);
+                dP = mma_p1_pad_reg<T, D, DT>(rows16(qi[buf][QI_DL], mt), Dt, 32 * mt + c, g, vreg);
                 float X[16];
                 if (diag) diag_x_queries(X, r, phiblk, mt, sr, g);  // X_ts = min phi(s, t] in the block
                 if (!diag) {
@@ -260,7 +223,7 @@ fpa_bwd_kv_kernel(BwdParams p) {
                     // every key; rows of a ragged last block are past T and have P = 0.
                     auto offdiag = [&](auto prod_c) {
                         constexpr bool PROD = decltype(prod_c)::value;
-                        const float *rZQ = qi[buf][5];
+                        const float *rZQ = qi[buf][QI_ZQ];
 #pragma unroll
                         for (int jq = 0; jq < 4; ++jq) {
                             const int t4 = 32 * mt + 8 * jq + 4 * g;

@@ -85,7 +85,7 @@ fpa_bwd_q_kernel(BwdParams p) {
     float lse = pinf(), del = 0.f, pre = 0.f, prel = 0.f;
     if (t_valid) {
         lse = p.lse[rowbase + tq];
-        del = p.qinfo[qi_at(bh, p.NB, tq, QI_DEL)];
+        del = -p.qinfo[qi_at(bh, p.NB, tq, QI_DL)];
         pre = p.state[L.at(PL_PRE, bh, tq)];
         prel = p.state[L.at(PL_PREL, bh, tq)];
     }
@@ -93,39 +93,14 @@ fpa_bwd_q_kernel(BwdParams p) {
     const float prel_ct = fexp2(prel - ct);
     const float E = (betal >= 0.f) ? ninf() : pinf();  // med3(x, y, E) = min (beta >= 0) or max (beta < 0)
 
-    // One more contraction step folds -lse_t into S and -Delta_t into dP: the key side's operand
-    // is {2^k, 2^k} (first two of its 16 entries), the query side's {-hi, -lo} with
-    // hi + lo = (lse / sc2) / 2^k (resp. Delta / 2^k) in fp16; k (per wave, usually 0) keeps
-    // hi within fp16 range.  fp32 operands carry the value in one entry.  Rows past T get
-    // lse = +inf, which becomes a -inf score (P = 0).
-    typename MT<T>::op_t kone_s, kone_d, qaug, daug;
-    if constexpr (sizeof(T) == 2) {
-        const f16 zero = (f16)0.f;
-        const h8 z8 = {zero, zero, zero, zero, zero, zero, zero, zero};
-        auto pow2_scale = [&](float x) {  // smallest 2^k (k <= 15) with max |x| / 2^k below 16384
-            float m = (__float_as_uint(x) & 0x7f800000u) == 0x7f800000u ? 0.f : fabsf(x);
+    // The S and dP accumulators start at -lse_t / sc2 and -Delta_t (this lane's query, the same in
+    // all 16 registers): the MFMA chains subtract them for free.  Rows past T get lse = +inf, so
+    // their scores are -inf and P = 0 with no per-element mask.
+    f32x16 lq16, dl16;
 #pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-            float sc = 1.f;
-            for (int k = 0; k < 15 && m >= 16384.f * sc; ++k) sc *= 2.f;
-            return uniform_f(sc);
-        };
-        auto fold = [&](float x, float sc) {
-            const float xs = x / sc;
-            const f16 hi = (f16)xs;
-            const f16 lo = ((__float_as_uint(xs) & 0x7f800000u) == 0x7f800000u) ? zero : (f16)(xs - (float)hi);
-            return h8{(f16)-hi, (f16)-lo, zero, zero, zero, zero, zero, zero};
-        };
-        const float lq = lse / p.sc2;
-        const float scl = pow2_scale(lq), scd = pow2_scale(del);
-        kone_s = g ? z8 : h8{(f16)scl, (f16)scl, zero, zero, zero, zero, zero, zero};
-        kone_d = g ? z8 : h8{(f16)scd, (f16)scd, zero, zero, zero, zero, zero, zero};
-        qaug = g ? z8 : fold(lq, scl);
-        daug = g ? z8 : fold(del, scd);
-    } else {
-        kone_s = kone_d = g ? 0.f : 1.f;
-        qaug = g ? 0.f : -lse / p.sc2;
-        daug = g ? 0.f : -del;
+    for (int j = 0; j < 16; ++j) {
+        lq16[j] = -lse / p.sc2;
+        dl16[j] = -del;
     }
 
     f32x16 dqacc[NDT];
@@ -176,8 +151,8 @@ fpa_bwd_q_kernel(BwdParams p) {
 #pragma unroll 1
             for (int mt = 1; mt >= 0; --mt) {
                 // S' = S - lse_t / sc2 and dP' = dP - Delta_t  ([s][t])
-                f32x16 S = MT<T>::mma(kone_s, qaug, mma_p1_pad_reg<T, D, DT>(zero16(), Kt, 32 * mt + c, g, qreg));
-                f32x16 dP = MT<T>::mma(kone_d, daug, mma_p1_pad_reg<T, D, DT>(zero16(), Vt, 32 * mt + c, g, doreg));
+                f32x16 S = mma_p1_pad_reg<T, D, DT>(lq16, Kt, 32 * mt + c, g, qreg);
+                f32x16 dP = mma_p1_pad_reg<T, D, DT>(dl16, Vt, 32 * mt + c, g, doreg);
                 float X[16];
                 if (diag) diag_x_keys(X, r, kPHI, mt, tr, g);  // X_ts = min phi(s, t] in the block
                 if (!diag) {

@@ -61,15 +61,11 @@ struct BwdParams {
 };
 
 // BwdParams::qinfo holds, per 64-query block of a head, QI_PLANES planes of 64 floats
-// ([bh][block][plane][64]), so the key side stages a block with two 1 KB loads.  QI_L and QI_D
-// span two planes each: the pair of 32-bit words of row r sits at 2 (r % 64) of that span.
-// QI_BST holds the block's BMIN and BLSE at positions 0 and 1.
-enum { QI_L = 0, QI_D = 2, QI_BPRE = 4, QI_ZQ = 5, QI_DEL = 6, QI_BST = 7, QI_PLANES = 8 };
+// ([bh][block][plane][64]), so the key side stages a block's first four planes with one 1 KB load.
+// QI_BST holds the block's BMIN and BLSE at positions 0 and 1; planes 5-7 are unused.
+enum { QI_LQ = 0, QI_DL = 1, QI_BPRE = 2, QI_ZQ = 3, QI_BST = 4, QI_PLANES = 8 };
 __host__ __device__ inline int64_t qi_at(int64_t bh, int NB, int row, int plane) {
     return ((bh * NB + row / 64) * QI_PLANES + plane) * 64 + row % 64;
-}
-__host__ __device__ inline int64_t qi_pair_at(int64_t bh, int NB, int row, int plane) {
-    return ((bh * NB + row / 64) * QI_PLANES + plane) * 64 + 2 * (row % 64);
 }
 
 // Launchers (defined next to their kernels); return hipSuccess or the launch error.
