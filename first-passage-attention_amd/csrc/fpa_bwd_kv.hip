@@ -259,7 +259,7 @@ fpa_bwd_kv_kernel(BwdParams p) {
                         for (int e = 0; e < 4; ++e) {
                             const int j = 4 * jq + e;
                             const int t = ib * BQ + t4 + e;
-                            const bool valid = (t >= s) && s_valid;  // rows past T: lse = +inf gives P = 0
+                            const bool valid = (t >= s) && s_valid;  // rows past T have -inf scores: P = 0
                             const bool strict = valid && (t > s);
                             const float x = X[j] - psi_s;
                             const float bm = strict ? beff * fminf(x, 0.f) : 0.f;  // x is +inf where the range is empty

@@ -81,7 +81,6 @@ fpa_bwd_q_kernel(BwdParams p) {
     load_row_p1<T, D>(doreg, DOb + (int64_t)tq * p.sdo.t, t_valid, g);
 
     const float betal = p.beta[h] * LOG2E;
-    // Rows past T: lse = +inf makes P = 0 with no per-element mask.
     float lse = pinf(), del = 0.f, pre = 0.f, prel = 0.f;
     if (t_valid) {
         lse = p.lse[rowbase + tq];

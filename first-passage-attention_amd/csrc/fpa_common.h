@@ -168,26 +168,6 @@ __device__ __forceinline__ f32x16 mma_p1_lds_reg(f32x16 acc, const T *arow, int 
     return acc;
 }
 
-// acc += A * B over a contraction of length K, both operands P1 rows in LDS.
-template <typename T, int K>
-__device__ __forceinline__ f32x16 mma_p1_lds_lds(f32x16 acc, const T *arow, const T *brow, int g) {
-    if constexpr (sizeof(T) == 2) {
-#pragma unroll
-        for (int i = 0; i < K / 16; ++i)
-            acc = MT<T>::mma(*reinterpret_cast<const h8 *>(arow + 16 * i + 8 * g),
-                             *reinterpret_cast<const h8 *>(brow + 16 * i + 8 * g), acc);
-    } else {
-#pragma unroll
-        for (int i = 0; i < K / 8; ++i) {
-            const f32x4 a = *reinterpret_cast<const f32x4 *>(arow + g * (K / 2) + 4 * i);
-            const f32x4 b = *reinterpret_cast<const f32x4 *>(brow + g * (K / 2) + 4 * i);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc = MT<T>::mma(a[e], b[e], acc);
-        }
-    }
-    return acc;
-}
-
 // ---------------------------------------------------------------------------
 // P3 operands read from a natural-layout LDS tile X[krow][n] (pitch in elements).
 //
@@ -322,7 +302,7 @@ __device__ __forceinline__ float max_halves(float x) {
 // A tile holds NR rows of DT elements (DT = D rounded up to 32) at a pitch of DT + one
 // 16-byte chunk: row r starts at byte r * ROWB, so every LDS read of a lane is a per-lane
 // base plus an immediate offset, and a 16-lane group reading one chunk column touches 16
-// distinct bank groups (ROWB / 16 is odd).  global_load_lds_dwordx4 writes the 16 bytes of
+// distinct bank groups (ROWB / 16 is odd).  An LDS-direct buffer load writes the 16 bytes of
 // lane l of a wave to (LDS base + 16 * l): each wave instruction fills 64 consecutive
 // chunk slots of the tile, and each lane fetches the global chunk that belongs in its
 // slot.  Pad slots and the chunks of columns D..DT-1 fetch a real chunk of the same row
@@ -330,7 +310,6 @@ __device__ __forceinline__ float max_halves(float x) {
 // (finite values that the callers mask).
 // ---------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void gbl_void_t;
 
 template <typename T, int DT> struct Pad {
     static constexpr int CE = 16 / sizeof(T);  // elements per chunk
@@ -340,10 +319,6 @@ template <typename T, int DT> struct Pad {
     static constexpr int ROWB = PITCH * sizeof(T);
     template <int NR> static constexpr int bytes() { return NR * ROWB; }
 };
-
-__device__ __forceinline__ void gl_lds16(const void *src, void *lds_dst) {
-    __builtin_amdgcn_global_load_lds((gbl_void_t *)(src), (lds_void_t *)(lds_dst), 16, 0, 0);
-}
 
 // Raw buffer resource (SGPRs) over bytes [base, base + 2^31) of a wave-uniform pointer.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base) {
@@ -456,46 +431,6 @@ __device__ __forceinline__ f32x16 mma_p2_p3_pad(f32x16 acc, const f32x16 &c0, co
     return mma_p2_p3<T, 1, A_IS_P3>(acc, c, reinterpret_cast<const T *>(tile) + row0 * Pad<T, DT>::PITCH,
                                     Pad<T, DT>::PITCH, ncol0, lane);
 }
-
-// ---------------------------------------------------------------------------
-// Register prefetch of an NR x D tile of a (B, H, T, D)-strided tensor (rows row0 + r,
-// zero past T), stored afterwards into a natural-layout LDS tile of the given pitch.
-// ---------------------------------------------------------------------------
-template <typename T, int D, int NR, int NTH> struct TileRegs {
-    static constexpr int CE = MT<T>::CHUNK;
-    static constexpr int CPR = D / CE;
-    static constexpr int NCH = NR * CPR;
-    static constexpr int PER = (NCH + NTH - 1) / NTH;
-    f32x4 r[PER];
-    __device__ __forceinline__ void load(const T *base, int64_t st, int row0, int T_) {
-        if (row0 + NR <= T_ && NCH % NTH == 0) {  // full tile: no per-row guard
-#pragma unroll
-            for (int i = 0; i < PER; ++i) {
-                const int idx = threadIdx.x + i * NTH;
-                const int row = idx / CPR, cc = idx % CPR;
-                r[i] = *reinterpret_cast<const f32x4 *>(base + (int64_t)(row0 + row) * st + cc * CE);
-            }
-            return;
-        }
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int idx = threadIdx.x + i * NTH;
-            const int row = idx / CPR, cc = idx % CPR;
-            f32x4 v = {0.f, 0.f, 0.f, 0.f};
-            if (idx < NCH && row0 + row < T_)
-                v = *reinterpret_cast<const f32x4 *>(base + (int64_t)(row0 + row) * st + cc * CE);
-            r[i] = v;
-        }
-    }
-    __device__ __forceinline__ void store(T *dst, int pitch) const {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int idx = threadIdx.x + i * NTH;
-            const int row = idx / CPR, cc = idx % CPR;
-            if (idx < NCH) *reinterpret_cast<f32x4 *>(dst + row * pitch + cc * CE) = r[i];
-        }
-    }
-};
 
 // Register P1 operands of one global row (zeros when the row is past T).
 template <typename T, int D>
