@@ -270,14 +270,18 @@ def main():
 
     P = pairs(cfg)
     D = cfg["D"]
+    # The kernels of a step, with their algorithmic flops.  The backward's key side (S, dP, dV, dK:
+    # 8*D per pair) and query side (dQ: 2*D per pair; it recomputes S and dP) run as one launch.
     kernels = {
         "fpa_stats": (time_call(fa, _hip.run_fwd, _lib.FPA_FWD_STATS), 0),
         "fpa_fwd_kernel": (time_call(fa, _hip.run_fwd, _lib.FPA_FWD_MAIN), 4 * D * P),
         "fpa_bwd_prep": (time_call(ba, _hip.run_bwd, _lib.FPA_BWD_DELTA), 0),
-        "fpa_bwd_kv_kernel": (time_call(ba, _hip.run_bwd, _lib.FPA_BWD_KEYS), 8 * D * P),
-        "fpa_bwd_q_kernel": (time_call(ba, _hip.run_bwd, _lib.FPA_BWD_QUERIES), 2 * D * P),
+        "fpa_bwd_kvq_kernel": (time_call(ba, _hip.run_bwd, _lib.FPA_BWD_KEYS | _lib.FPA_BWD_QUERIES), 10 * D * P),
         "fpa_bwd_combine_kernel": (time_call(ba, _hip.run_bwd, _lib.FPA_BWD_PHI), 0),
     }
+    # Each side launched alone (not part of the step): for comparison with the fused launch.
+    alone = {"fpa_bwd_kv_kernel": time_call(ba, _hip.run_bwd, _lib.FPA_BWD_KEYS),
+             "fpa_bwd_q_kernel": time_call(ba, _hip.run_bwd, _lib.FPA_BWD_QUERIES)}
     dom = max(kernels, key=lambda n: kernels[n][0])
     dom_ms, dom_flops = kernels[dom]
     peak = PEAK_TFLOPS[cfg["dtype"]]
@@ -314,6 +318,7 @@ def main():
         "fwd_pct_peak": round(100 * fwd_tflops / peak, 2),
         "fwd_bwd_pct_peak": round(100 * fb_tflops / peak, 2),
         "kernel_ms": {n: round(t, 4) for n, (t, _) in kernels.items()},
+        "kernel_ms_alone": {n: round(t, 4) for n, t in alone.items()},
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 3), "peak": peak,
                      "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
                      "traffic": measured_traffic(a.config, dom)},

@@ -178,10 +178,14 @@ int fpa_bwd(const FpaBwdArgs *a, void *stream) {
     hipError_t e;
     if ((ph & FPA_BWD_DELTA) && (e = launch_bwd_prep(p, a->dtype, (int)a->D, s)) != hipSuccess)
         return hip_fail(e, "fpa_bwd_prep launch");
-    if ((ph & FPA_BWD_KEYS) && (e = launch_bwd_kv(p, a->dtype, (int)a->D, s)) != hipSuccess)
-        return hip_fail(e, "fpa_bwd_kv launch");
-    if ((ph & FPA_BWD_QUERIES) && (e = launch_bwd_q(p, a->dtype, (int)a->D, s)) != hipSuccess)
-        return hip_fail(e, "fpa_bwd_q launch");
+    if ((ph & FPA_BWD_KEYS) && (ph & FPA_BWD_QUERIES)) {
+        if ((e = launch_bwd_kvq(p, a->dtype, (int)a->D, s)) != hipSuccess) return hip_fail(e, "fpa_bwd_kvq launch");
+    } else {
+        if ((ph & FPA_BWD_KEYS) && (e = launch_bwd_kv(p, a->dtype, (int)a->D, s)) != hipSuccess)
+            return hip_fail(e, "fpa_bwd_kv launch");
+        if ((ph & FPA_BWD_QUERIES) && (e = launch_bwd_q(p, a->dtype, (int)a->D, s)) != hipSuccess)
+            return hip_fail(e, "fpa_bwd_q launch");
+    }
     if ((ph & (FPA_BWD_PHI | FPA_BWD_BETA)) && (e = launch_bwd_combine(p, s)) != hipSuccess)
         return hip_fail(e, "fpa_bwd_combine launch");
     return FPA_OK;

@@ -82,8 +82,8 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
     __shared__ float contrib[G][G + 1];      // [u][s]
     __shared__ float red[4];
 
-    const int U = blockIdx.x, bh = blockIdx.y, b = bh / p.H, h = bh % p.H;
-    const int tid = threadIdx.x, lane = tid % 64;
+    const int U = group_x(), bh = group_y(), b = bh / p.H, h = bh % p.H;
+    const int tid = thread_x(), lane = tid % 64;
     const int w = __builtin_amdgcn_readfirstlane(tid / 64);
     const int sb = U * G, last = min(G - 1, p.T - 1 - sb);
     const StateLayout L{p.BH, p.TP, p.NB};

@@ -1,0 +1,303 @@
+// fpa_bwd_kv.h -- the key-side backward tile of First Passage Attention.
+//
+// Reference behaviour: _bwd_kv (kernel.py:177-265) of yliu-fort/first-passage-attention.
+// gfx950 design: a workgroup of FPA_NW waves owns
+// 32 keys per wave (one key per lane column) and streams 64-query blocks from the
+// diagonal to T through double-buffered, padded LDS tiles filled by direct global->LDS
+// loads (one barrier per block).  Each wave computes S = Q K^T and dP = dO V^T with K, V
+// held in registers, then dV^T += dO^T P and dK^T += Q^T dS on the 32x32 MFMA (dO^T
+// and Q^T read from the row-major tiles with LDS transpose reads).  Per key it reduces
+//   dpsi_s  = -beta * sum_t g_ts                       (g = [x <= 0] dS, strict t > s)
+//   dbeta   = sum_{t>s} dS_ts min(0, x_ts)             (per-wave partials, summed later)
+//   W_s     = sum_{t outside blk(s)} g_ts 2^{C_s} / Z_ts   (key-block soft-min sums)
+//   TBUF    = middle-block soft-min sums per (query block, key block, key half)
+// and writes the in-block gated dS to GD for the in-block soft-min recurrence.
+#pragma once
+
+#include <type_traits>
+
+#include "fpa_common.h"
+#include "fpa_params.h"
+
+// Tuning knobs (build-time): waves per SIMD of the fp16 D <= 64 key-side kernel, and whether
+// well-conditioned tiles use the shared-reference soft-min path.
+#ifndef FPA_KV_WPE
+#define FPA_KV_WPE 2
+#endif
+#ifndef FPA_KV_PROD
+#define FPA_KV_PROD 1
+#endif
+
+namespace fpa {
+
+// Per-query planes of the backward (QI_*), for t < TP:
+//   LQ    -lse_t / sc2 (-inf past T) and DL = -Delta_t (0 past T), Delta_t = sum_d dO_td O_td: the
+//         start values of the S and dP accumulators, so the MFMA chains subtract them for free;
+//         rows past T get -inf scores and P = 0 with no per-element mask
+//   BPRE  beff * PRE_t (beff = beta * log2e, or 2^-100 for beta = 0; +-inf past T)
+//   ZQ    with PRL_t = PREL_t - BLSE <= 0 (BLSE = log2 sum 2^a over t's block; 0 past T):
+//         2^{PRL_t} > 0 when the block's spread -PRL_{first row} is at most PROD_SPREAD
+//         (product form of the soft-min denominators), else PRL_t <= 0 (exact form).  The sign
+//         of the block's first entry tells the two apart.
+//   BST   the block's BMIN and BLSE (positions 0 and 1).
+__device__ __forceinline__ float beta_eff(float betal) { return betal != 0.f ? betal : 0x1p-100f; }
+
+// Waves per SIMD of the key-side tile: wide tiles need the registers of one wave per SIMD.
+template <typename T, int D>
+constexpr int kv_wpe() { return (D >= 128 || (sizeof(T) == 4 && D >= 64)) ? 1 : FPA_KV_WPE; }
+
+// LDS of one key-side workgroup.
+template <typename T, int D, int NW>
+struct KvShared {
+    static constexpr int TB = Pad<T, (D < 32 ? 32 : D)>::template bytes<64>();  // one padded Q or dO tile
+    __attribute__((aligned(1024))) char Qs[2][TB];
+    __attribute__((aligned(1024))) char dOs[2][TB];
+    __attribute__((aligned(1024))) float qi[2][5][64];  // per-query values of a block: LQ, DL, BPRE, ZQ, BST
+    __attribute__((aligned(16))) float kPHI[32 * NW];
+};
+
+// Keys [32 NW kt, 32 NW (kt + 1)) of head bh: every query block from the keys' diagonal block to T.
+template <typename T, int D, int NW>
+__device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, NW> &sm, const int kt, const int bh) {
+    constexpr int BK = 32 * NW, BQ = 64;   // keys per workgroup, queries per iteration (one block)
+    constexpr int DT = D < 32 ? 32 : D;
+    constexpr int NDT = DT / 32;
+    auto &Qs = sm.Qs;
+    auto &dOs = sm.dOs;
+    auto &qi = sm.qi;
+    float *const kPHI = sm.kPHI;
+
+    const int tid = thread_x(), lane = tid % 64, g = lane / 32, c = lane % 32;
+    const int w = __builtin_amdgcn_readfirstlane(tid / 64);  // wave index, uniform across the wave
+    const int b = bh / p.H, h = bh % p.H;
+    const int k0 = kt * BK, kw0 = k0 + 32 * w, s = kw0 + c;
+    const int jb = kw0 / G, sb = jb * G;
+    const bool wave_active = kw0 < p.T;
+    const bool s_valid = s < p.T;
+    const StateLayout L{p.BH, p.TP, p.NB};
+    const int64_t rowbase = (int64_t)bh * p.TP;
+    const int64_t brow = (int64_t)bh * p.NB;
+
+    const T *Qb = static_cast<const T *>(p.q) + b * p.sq.b + h * p.sq.h;
+    const T *Kb = static_cast<const T *>(p.k) + b * p.sk.b + h * p.sk.h;
+    const T *Vb = static_cast<const T *>(p.v) + b * p.sv.b + h * p.sv.h;
+    const T *DOb = static_cast<const T *>(p.dout) + b * p.sdo.b + h * p.sdo.h;
+    // A block's per-query values: planes 0-3 (LQ, DL, BPRE, ZQ) with one 1 KB load, BST with a 256 B one.
+    const float *qi_head = p.qinfo + qi_at(bh, p.NB, 0, 0);
+
+    TileLoader<T, D, DT, BQ, NW> qld, dld;
+    qld.init(p.sq.t, w, lane);
+    dld.init(p.sdo.t, w, lane);
+    auto issue = [&](int ib, int buf) {
+        qld.issue(Qs[buf], Qb, p.sq.t, ib * BQ, p.T, w, lane);
+        dld.issue(dOs[buf], DOb, p.sdo.t, ib * BQ, p.T, w, lane);
+        if (w == NW - 1) buf_lds16(buf_rsrc(qi_head + (int64_t)ib * QI_PLANES * 64), 16 * lane, &qi[buf][0][0]);
+        if (w == (NW >= 2 ? NW - 2 : 0))
+            buf_lds4(buf_rsrc(qi_head + (int64_t)ib * QI_PLANES * 64), 4 * (QI_BST * 64 + lane), &qi[buf][4][0]);
+    };
+    const int ib0 = k0 / G;
+    issue(ib0, 0);
+
+    OpRow<T, D> kreg, vreg;
+    load_row_p1<T, D>(kreg, Kb + (int64_t)s * p.sk.t, s_valid, g);
+    load_row_p1<T, D>(vreg, Vb + (int64_t)s * p.sv.t, s_valid, g);
+
+    // Bias terms scaled by beff = beta * log2e (2^-100 for beta = 0, below fp32 resolution in the
+    // exponent): v = beff * x with x = min(SUF_s, MID, PRE_t) - psi_s, bm = beff * min(x, 0) =
+    // med3(v, 0, E), and the gate x <= 0 is bm == v for either sign of beta.
+    const float beta = p.beta[h], beff = beta_eff(beta * LOG2E);
+    const float E = (beff > 0.f) ? ninf() : pinf();  // med3(x, y, E) = min (beff > 0) or max
+    float psi_s = 0.f, suf = pinf(), sufl = ninf();
+    if (s < p.TP) {
+        psi_s = p.state[L.at(PL_PSI, bh, s)];
+        suf = p.state[L.at(PL_SUF, bh, s)];
+        sufl = p.state[L.at(PL_SUFL, bh, s)];
+    }
+    const float Cs = (suf < pinf()) ? -suf * p.il2 : ninf();  // max a over (s, end of block)
+    const float bsuf = beff * suf, bpsi = beff * psi_s;
+    // Accumulator start values from a per-query plane of the staged block: register j of this
+    // lane holds row 32 mt + 8 (j / 4) + 4 g + j % 4.
+    auto rows16 = [&](const float *plane, int mt) {
+        f32x16 r;
+#pragma unroll
+        for (int jq = 0; jq < 4; ++jq) {
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(&plane[32 * mt + 8 * jq + 4 * g]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) r[4 * jq + e] = v[e];
+        }
+        return r;
+    };
+    if (tid < BK) kPHI[tid] = (k0 + tid < p.TP) ? p.state[L.at(PL_PHI, bh, k0 + tid)] : pinf();
+
+    f32x16 dkacc[NDT], dvacc[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+        dkacc[dt] = zero16();
+        dvacc[dt] = zero16();
+    }
+    float gsum = 0.f, dbacc = 0.f, Wacc = 0.f;
+    float mid = pinf(), midl = ninf(), cmid = ninf();  // over blocks strictly between jb and ib
+    const float *phiblk = kPHI + (sb - k0);
+
+    // Block statistics used by a query block, loaded one block ahead: BMIN / BLSE of block
+    // ib - 1 (which joins the middle) and BLSE of block ib.
+    float bm_prev = 0.f, bl_prev = 0.f;  // block ib - 1, from the previous block's staged values
+    wait_loads();
+    __syncthreads();
+    for (int ib = ib0, it = 0; ib < p.NB; ++ib, ++it) {
+        const int buf = it & 1;
+        if (ib + 1 < p.NB) issue(ib + 1, buf ^ 1);
+        const float bm_here = qi[buf][QI_BST][0], bl_cur = qi[buf][QI_BST][1];  // block ib
+        if (wave_active && ib >= jb) {
+            // Soft-min denominators off the diagonal: Z_ts 2^{-rs} = sv + 2^{PREL_t - rs} with the
+            // per-key reference rs = max(C_s, cmid) (sv >= 1 when rs is finite).  With
+            // rsb = rs - BLSE, 2^{PREL_t - rs} = 2^{PRL_t - rsb}; when the block's PRL spread is at
+            // most PROD_SPREAD this is ZQ_t * ck with ZQ_t = 2^{PRL_t} and ck = 2^{min(-rsb, 126)}:
+            // one FMA per element instead of an exp2.  The clamp only changes terms whose
+            // 2^{PREL_t - rs} exceeds 2^{126 - PROD_SPREAD}, where 1/Z is already below 2^{-26} of
+            // the other terms.
+            float rs = ninf(), rsb = ninf(), sv = 0.f, ck = 0.f;
+            bool prod = false;
+            if (ib > jb) {
+                if (ib - 1 > jb) {  // block ib - 1 joins the middle
+                    mid = fminf(mid, bm_prev);
+                    midl = lse2_pair(midl, bl_prev);
+                    cmid = fmaxf(cmid, -bm_prev * p.il2);
+                }
+                rs = fmaxf(Cs, cmid);
+                sv = (rs > ninf()) ? fexp2(sufl - rs) + fexp2(midl - rs) : 0.f;
+                rsb = rs - bl_cur;
+                ck = fexp2(fminf(-rsb, 126.f));
+                prod = uniform_f(qi[buf][QI_ZQ][0]) > 0.f;
+            }
+            const float cA = __builtin_amdgcn_fmed3f(bsuf, beff * mid, E);  // beff * min(SUF_s, MID)
+            const char *Qt = Qs[buf];
+            const char *Dt = dOs[buf];
+            const float *rBPRE = qi[buf][QI_BPRE];
+            const bool diag = (ib == jb);
+            const int sr = s - sb;
+            float r = pinf();  // running min of phi over (s, u] for the in-block scan
+            float wblk = 0.f;
+#pragma unroll 1
+            for (int mt = 0; mt < 2; ++mt) {
+                f32x16 S, dP;
+                // S - lse / sc2 and dP - Delta, rows t, columns s
+                S = mma_p1_pad_reg<T, D, DT>(rows16(qi[buf][QI_LQ], mt), Qt, 32 * mt + c, g, kreg);
+                dP = mma_p1_pad_reg<T, D, DT>(rows16(qi[buf][QI_DL], mt), Dt, 32 * mt + c, g, vreg);
+                float X[16];
+                if (diag) diag_x_queries(X, r, phiblk, mt, sr, g);  // X_ts = min phi(s, t] in the block
+                if (!diag) {
+                    // Off the diagonal block every key is valid and every query is later than
+                    // every key; rows of a ragged last block are past T and have P = 0.
+                    auto offdiag = [&](auto prod_c) {
+                        constexpr bool PROD = decltype(prod_c)::value;
+                        const float *rZQ = qi[buf][QI_ZQ];
+#pragma unroll
+                        for (int jq = 0; jq < 4; ++jq) {
+                            const int t4 = 32 * mt + 8 * jq + 4 * g;
+                            const f32x4 bpre4 = *reinterpret_cast<const f32x4 *>(&rBPRE[t4]);
+                            const f32x4 zq4 = *reinterpret_cast<const f32x4 *>(&rZQ[t4]);
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                const int j = 4 * jq + e;
+                                const float v = __builtin_amdgcn_fmed3f(cA, bpre4[e], E) - bpsi;
+                                const float bm = __builtin_amdgcn_fmed3f(v, 0.f, E);
+                                const float P = fexp2(fmaf(S[j], p.sc2, bm));
+                                const float dS = P * dP[j];
+                                const float gg = (bm == v) ? dS : 0.f;
+                                gsum += gg;
+                                dbacc = fmaf(dS, bm, dbacc);
+                                const float z = PROD ? fmaf(zq4[e], ck, sv) : sv + fexp2(zq4[e] - rsb);
+                                wblk = fmaf(gg, frcp(z), wblk);
+                                S[j] = P;
+                                dP[j] = dS;
+                            }
+                        }
+                    };
+                    if (prod)
+                        offdiag(std::true_type{});
+                    else
+                        offdiag(std::false_type{});
+                } else {
+#pragma unroll
+                    for (int jq = 0; jq < 4; ++jq) {
+                        const int t4 = 32 * mt + 8 * jq + 4 * g;
+                        f32x4 g4;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int j = 4 * jq + e;
+                            const int t = ib * BQ + t4 + e;
+                            const bool valid = (t >= s) && s_valid;  // rows past T have -inf scores: P = 0
+                            const bool strict = valid && (t > s);
+                            const float x = X[j] - psi_s;
+                            const float bm = strict ? beff * fminf(x, 0.f) : 0.f;  // x is +inf where the range is empty
+                            const float P = valid ? fexp2(fmaf(S[j], p.sc2, bm)) : 0.f;
+                            const float dS = P * dP[j];
+                            const float gg = (strict && x <= 0.f) ? dS : 0.f;
+                            gsum += gg;
+                            dbacc = fmaf(dS, bm, dbacc);
+                            g4[e] = gg;
+                            S[j] = P;
+                            dP[j] = dS;
+                        }
+                        if (s_valid) *reinterpret_cast<f32x4 *>(p.gd + ((brow + jb) * G + sr) * G + t4) = g4;
+                    }
+                }
+                // dV^T[d][s] += dO^T[d][t] P[t][s];  dK^T[d][s] += Q^T[d][t] dS[t][s]
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) {
+                    dvacc[dt] = mma_p2_p3_pad<T, DT, true>(dvacc[dt], S, Dt, 32 * mt, 32 * dt, lane);
+                    dkacc[dt] = mma_p2_p3_pad<T, DT, true>(dkacc[dt], dP, Qt, 32 * mt, 32 * dt, lane);
+                }
+            }
+            if (ib > jb) {  // close query block ib: key-block and middle-block soft-min sums
+                if (rs > ninf()) Wacc = fmaf(fexp2(Cs - rs), wblk, Wacc);
+                if (ib > jb + 1) {
+                    const float tp = wave_sum((rs > ninf()) ? fexp2(cmid - rs) * wblk : 0.f);
+                    if (lane == 0) p.tbuf[((brow + ib) * p.NB + jb) * 2 + ((kw0 / 32) & 1)] = tp;
+                }
+            }
+        }
+        bm_prev = bm_here;
+        bl_prev = bl_cur;
+        wait_loads();
+        __syncthreads();
+    }
+
+    // Per-key outputs (lanes c and c + 32 hold the same key, different queries).
+    gsum = sum_halves(gsum);
+    Wacc = sum_halves(Wacc);
+    const float dbw = wave_sum(dbacc) / beff;
+    if (!wave_active) return;
+    if (lane == 0) p.dbp[(int64_t)bh * p.NK32 + kw0 / 32] = dbw;  // one partial per 32-key group
+    if (g == 0 && s < p.TP) p.wsum[rowbase + s] = Wacc;
+    if (g == 0 && s_valid) p.dpsi[(int64_t)bh * p.T + s] = -beta * gsum;
+    if (!s_valid) return;
+    T *dKr = static_cast<T *>(p.dk) + b * p.sdk.b + h * p.sdk.h + (int64_t)s * p.sdk.t;
+    T *dVr = static_cast<T *>(p.dv) + b * p.sdv.b + h * p.sdv.h + (int64_t)s * p.sdv.t;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int jq = 0; jq < 4; ++jq) {
+            const int d0 = 32 * dt + 8 * jq + 4 * g;
+            if (d0 < D) {
+                if constexpr (sizeof(T) == 2) {
+                    h4 kv4 = {(f16)(dkacc[dt][4 * jq + 0] * p.smscale), (f16)(dkacc[dt][4 * jq + 1] * p.smscale),
+                              (f16)(dkacc[dt][4 * jq + 2] * p.smscale), (f16)(dkacc[dt][4 * jq + 3] * p.smscale)};
+                    h4 vv4 = {(f16)dvacc[dt][4 * jq + 0], (f16)dvacc[dt][4 * jq + 1], (f16)dvacc[dt][4 * jq + 2],
+                              (f16)dvacc[dt][4 * jq + 3]};
+                    *reinterpret_cast<h4 *>(dKr + d0) = kv4;
+                    *reinterpret_cast<h4 *>(dVr + d0) = vv4;
+                } else {
+                    f32x4 kv4 = {dkacc[dt][4 * jq + 0] * p.smscale, dkacc[dt][4 * jq + 1] * p.smscale,
+                                 dkacc[dt][4 * jq + 2] * p.smscale, dkacc[dt][4 * jq + 3] * p.smscale};
+                    f32x4 vv4 = {dvacc[dt][4 * jq + 0], dvacc[dt][4 * jq + 1], dvacc[dt][4 * jq + 2],
+                                 dvacc[dt][4 * jq + 3]};
+                    *reinterpret_cast<f32x4 *>(dKr + d0) = kv4;
+                    *reinterpret_cast<f32x4 *>(dVr + d0) = vv4;
+                }
+            }
+        }
+}
+
+}  // namespace fpa

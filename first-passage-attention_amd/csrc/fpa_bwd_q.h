@@ -1,0 +1,258 @@
+// fpa_bwd_q.h -- the query-side backward tile of First Passage Attention.
+//
+// Reference behaviour: _bwd_q (kernel.py:286-340) of yliu-fort/first-passage-attention.
+// gfx950 design: a workgroup of FPA_NW waves owns 32 queries per wave (one query per lane
+// column) and streams 64-key blocks from the diagonal down to key 0 through
+// double-buffered, padded LDS tiles filled by direct global->LDS loads (one barrier per
+// block).  Each wave
+// recomputes S^T = K Q^T and dP^T = V dO^T with Q, dO in registers, accumulates
+// dQ^T += K^T dS^T on the 32x32 MFMA (K^T read from the row-major tile with LDS
+// transpose reads), and reduces per query the query-block soft-min sum
+//   R_t = sum_{s outside blk(t)} g_ts 2^{c_t} / Z_ts,   c_t = max a over [start of blk(t), t].
+// The diagonal block (keys and query in one 64-block) uses the in-block range minimum.
+#pragma once
+
+#include <type_traits>
+
+#include "fpa_common.h"
+#include "fpa_params.h"
+
+// Tuning knobs (build-time): waves per SIMD of the D <= 64 query-side kernel, and whether
+// well-conditioned tiles use the shared-reference soft-min path.
+#ifndef FPA_Q_WPE
+#define FPA_Q_WPE 2
+#endif
+#ifndef FPA_Q_FAST
+#define FPA_Q_FAST 1
+#endif
+
+namespace fpa {
+
+// Waves per SIMD of the query-side tile.
+template <typename T, int D>
+constexpr int q_wpe() { return (D >= 128) ? 1 : FPA_Q_WPE; }
+
+// LDS of one query-side workgroup.
+template <typename T, int D, int NW>
+struct QShared {
+    static constexpr int TB = Pad<T, (D < 32 ? 32 : D)>::template bytes<64>();  // one padded K or V tile
+    __attribute__((aligned(1024))) char Ks[2][TB];
+    __attribute__((aligned(1024))) char Vs[2][TB];
+    // Per-key values of a block: BSUF, CP (= betal * psi), SUFL, PHI, and BST (BMIN, BLSE, SUF of the
+    // first key at [4][0..2]).
+    __attribute__((aligned(1024))) float kst[2][5][64];
+    __attribute__((aligned(16))) float Aw[NW][64];  // per-wave key factors of the shared-reference path
+};
+
+// Queries [32 NW qt, 32 NW (qt + 1)) of head bh: every key block from their diagonal block down to 0.
+template <typename T, int D, int NW>
+__device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW> &sm, const int qt, const int bh) {
+    constexpr int BM = 32 * NW, BK = 64;  // queries per workgroup, keys per iteration (one block)
+    constexpr int DT = D < 32 ? 32 : D;
+    constexpr int NDT = DT / 32;
+    auto &Ks = sm.Ks;
+    auto &Vs = sm.Vs;
+    auto &kst = sm.kst;
+    auto &Aw = sm.Aw;
+
+    const int tid = thread_x(), lane = tid % 64, g = lane / 32, c = lane % 32;
+    const int w = __builtin_amdgcn_readfirstlane(tid / 64);  // wave index, uniform across the wave
+    const int b = bh / p.H, h = bh % p.H;
+    const int q0 = qt * BM, qw0 = q0 + 32 * w, tq = qw0 + c;
+    const int ib = qw0 / G;
+    const bool wave_active = qw0 < p.T;
+    const bool t_valid = tq < p.T;
+    const StateLayout L{p.BH, p.TP, p.NB};
+    const int64_t rowbase = (int64_t)bh * p.TP;
+    const int64_t brow = (int64_t)bh * p.NB;
+
+    const T *Qb = static_cast<const T *>(p.q) + b * p.sq.b + h * p.sq.h;
+    const T *Kb = static_cast<const T *>(p.k) + b * p.sk.b + h * p.sk.h;
+    const T *Vb = static_cast<const T *>(p.v) + b * p.sv.b + h * p.sv.h;
+    const T *DOb = static_cast<const T *>(p.dout) + b * p.sdo.b + h * p.sdo.h;
+    // lanes 0-15: BSUF, 16-31: CP, 32-47: SUFL, 48-63: PHI
+    const int kpl = (lane < 16) ? PL_BSUF : (lane < 32) ? PL_CP : (lane < 48) ? PL_SUFL : PL_PHI;
+    const float *st_head = p.state + L.at(0, bh, 0);
+    const uint32_t kst_off = (uint32_t)((kpl * p.TP + 4 * (lane & 15)) * 4);  // bytes from plane 0 of the head
+    const uint32_t bst_off = (uint32_t)((PL_BST * p.TP + lane) * 4);
+
+    TileLoader<T, D, DT, BK, NW> kld, vld;
+    kld.init(p.sk.t, w, lane);
+    vld.init(p.sv.t, w, lane);
+    auto issue = [&](int jb, int buf) {
+        kld.issue(Ks[buf], Kb, p.sk.t, jb * BK, p.T, w, lane);
+        vld.issue(Vs[buf], Vb, p.sv.t, jb * BK, p.T, w, lane);
+        if (w == NW - 1) buf_lds16(buf_rsrc(st_head + jb * BK), kst_off, &kst[buf][0][0]);
+        if (w == (NW >= 2 ? NW - 2 : 0)) buf_lds4(buf_rsrc(st_head + jb * BK), bst_off, &kst[buf][4][0]);
+    };
+    const int jbmax = umin_i(p.NB - 1, (q0 + BM - 1) / BK);
+    issue(jbmax, 0);
+
+    OpRow<T, D> qreg, doreg;
+    load_row_p1<T, D>(qreg, Qb + (int64_t)tq * p.sq.t, t_valid, g);
+    load_row_p1<T, D>(doreg, DOb + (int64_t)tq * p.sdo.t, t_valid, g);
+
+    const float betal = p.beta[h] * LOG2E;
+    float lse = pinf(), del = 0.f, pre = 0.f, prel = 0.f;
+    if (t_valid) {
+        lse = p.lse[rowbase + tq];
+        del = -p.qinfo[qi_at(bh, p.NB, tq, QI_DL)];
+        pre = p.state[L.at(PL_PRE, bh, tq)];
+        prel = p.state[L.at(PL_PREL, bh, tq)];
+    }
+    const float ct = -pre * p.il2;  // max a over [start of blk(t), t]
+    const float prel_ct = fexp2(prel - ct);
+    const float E = (betal >= 0.f) ? ninf() : pinf();  // med3(x, y, E) = min (beta >= 0) or max (beta < 0)
+
+    // The S and dP accumulators start at -lse_t / sc2 and -Delta_t (this lane's query, the same in
+    // all 16 registers): the MFMA chains subtract them for free.  Rows past T get lse = +inf, so
+    // their scores are -inf and P = 0 with no per-element mask.
+    f32x16 lq16, dl16;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        lq16[j] = -lse / p.sc2;
+        dl16[j] = -del;
+    }
+
+    f32x16 dqacc[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) dqacc[dt] = zero16();
+    float racc = 0.f;
+    float mid = pinf(), midl = ninf(), cmid = ninf();  // over blocks strictly between jb and ib
+    const int ibc = umin_i(ib, p.NB - 1);  // waves past T keep ib in range for these reads
+    const float a_first = -ld_uniform(p.state, L.at(PL_PHI, bh, ibc * G)) * p.il2;  // a of the block's first query
+    const float c_blk = -ld_uniform(p.state, L.bplane(BP_MIN) + brow + ibc) * p.il2;          // max a over block ib
+
+    // BMIN / BLSE of block jb + 1 (which joins the middle), from the previous block's staged values.
+    float bm_prev = 0.f, bl_prev = 0.f;
+    wait_loads();
+    __syncthreads();
+    for (int jb = jbmax, it = 0; jb >= 0; --jb, ++it) {
+        const int buf = it & 1;
+        const int s0 = jb * BK;
+        if (jb > 0) issue(jb - 1, buf ^ 1);
+        const float bm_here = kst[buf][4][0], bl_here = kst[buf][4][1], suf_first = kst[buf][4][2];
+        if (wave_active && jb <= ib) {
+            const float *kSUF = kst[buf][0], *kPSI = kst[buf][1], *kSUFL = kst[buf][2], *kPHI = kst[buf][3];
+            if (jb + 1 < ib) {  // block jb + 1 joins the middle
+                mid = fminf(mid, bm_prev);
+                midl = lse2_pair(midl, bl_prev);
+                cmid = fmaxf(cmid, -bm_prev * p.il2);
+            }
+            const float mterm = fexp2(midl - ct) + prel_ct;
+            // Shared reference R >= every exponent of the tile (largest C_s is at the block's first key).
+            bool fast = false;
+            float R = 0.f, bq = 0.f;
+            if (jb < ib) {
+                const float cfirst = -suf_first * p.il2;  // SUF of the block's first key
+                R = fmaxf(fmaxf(cfirst, cmid), c_blk);
+                fast = FPA_Q_FAST && (R - fmaxf(cmid, a_first)) < FAST_SPREAD;
+                if (fast) {
+                    Aw[w][lane] = fexp2(kSUFL[lane] - R) + fexp2(midl - R);
+                    bq = t_valid ? fexp2(prel - R) : 1.f;  // rows past T: any positive factor (g = 0)
+                }
+            }
+            float rblk = 0.f;  // sum of g / (Z 2^{-R}) over this key block (shared-reference path)
+            const float bY = betal * fminf(pre, mid);
+            const bool diag = (jb == ib);
+            const int tr = tq - s0;
+            const char *Kt = Ks[buf];
+            const char *Vt = Vs[buf];
+            float r = pinf();  // running min of phi over [u, t] for the in-block scan
+#pragma unroll 1
+            for (int mt = 1; mt >= 0; --mt) {
+                // S' = S - lse_t / sc2 and dP' = dP - Delta_t  ([s][t])
+                f32x16 S = mma_p1_pad_reg<T, D, DT>(lq16, Kt, 32 * mt + c, g, qreg);
+                f32x16 dP = mma_p1_pad_reg<T, D, DT>(dl16, Vt, 32 * mt + c, g, doreg);
+                float X[16];
+                if (diag) diag_x_keys(X, r, kPHI, mt, tr, g);  // X_ts = min phi(s, t] in the block
+                if (!diag) {
+                    // Off the diagonal block every key is valid and earlier than every query.
+                    auto offdiag = [&](auto fast_c) {
+                        constexpr bool FAST = decltype(fast_c)::value;
+#pragma unroll
+                        for (int jq = 0; jq < 4; ++jq) {
+                            const int s4 = 32 * mt + 8 * jq + 4 * g;
+                            const f32x4 bsuf4 = *reinterpret_cast<const f32x4 *>(&kSUF[s4]);
+                            const f32x4 bpsi4 = *reinterpret_cast<const f32x4 *>(&kPSI[s4]);
+                            const f32x4 zk4 = FAST ? *reinterpret_cast<const f32x4 *>(&Aw[w][s4])
+                                                   : *reinterpret_cast<const f32x4 *>(&kSUFL[s4]);
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                const int j = 4 * jq + e;
+                                // v = betal * x with x = min(SUF_s, MID, PRE_t) - psi_s, and the bias
+                                // bm = betal * min(x, 0); the gate x <= 0 is bm == v for either sign.
+                                const float v = __builtin_amdgcn_fmed3f(bsuf4[e], bY, E) - bpsi4[e];
+                                const float bm = __builtin_amdgcn_fmed3f(v, 0.f, E);
+                                const float P = fexp2(fmaf(S[j], p.sc2, bm));
+                                const float dS = P * dP[j];
+                                const float gg = (bm == v) ? dS : 0.f;
+                                if constexpr (FAST)
+                                    rblk = fmaf(gg, frcp(zk4[e] + bq), rblk);
+                                else
+                                    racc = fmaf(gg, frcp(fexp2(zk4[e] - ct) + mterm), racc);
+                                S[j] = dS;
+                            }
+                        }
+                    };
+#if FPA_Q_FAST
+                    if (fast)
+                        offdiag(std::true_type{});
+                    else
+#endif
+                        offdiag(std::false_type{});
+                } else {
+#pragma unroll
+                    for (int jq = 0; jq < 4; ++jq) {
+                        const int s4 = 32 * mt + 8 * jq + 4 * g;
+                        const f32x4 bpsi4 = *reinterpret_cast<const f32x4 *>(&kPSI[s4]);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int j = 4 * jq + e;
+                            const int s = s0 + s4 + e;
+                            const bool valid = t_valid && (s <= tq);
+                            const bool strict = valid && (s < tq);
+                            const float bm = strict ? __builtin_amdgcn_fmed3f(fmaf(betal, X[j], -bpsi4[e]), 0.f, E) : 0.f;
+                            const float P = valid ? fexp2(fmaf(S[j], p.sc2, bm)) : 0.f;
+                            S[j] = P * dP[j];
+                        }
+                    }
+                }
+                // dQ^T[d][t] += K^T[d][s] dS^T[s][t]   (K read transposed from its natural layout)
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt)
+                    dqacc[dt] = mma_p2_p3_pad<T, DT, true>(dqacc[dt], S, Kt, 32 * mt, 32 * dt, lane);
+            }
+            if (fast) racc = fmaf(fexp2(ct - R), rblk, racc);  // R_t gets 2^{c_t} sum g / Z
+        }
+        bm_prev = bm_here;
+        bl_prev = bl_here;
+        wait_loads();
+        __syncthreads();
+    }
+
+    racc = sum_halves(racc);
+    if (!wave_active) return;
+    if (g == 0 && tq < p.TP) p.rsum[rowbase + tq] = t_valid ? racc : 0.f;
+    if (!t_valid) return;
+    T *dQr = static_cast<T *>(p.dq) + b * p.sdq.b + h * p.sdq.h + (int64_t)tq * p.sdq.t;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int jq = 0; jq < 4; ++jq) {
+            const int d0 = 32 * dt + 8 * jq + 4 * g;
+            if (d0 < D) {
+                if constexpr (sizeof(T) == 2) {
+                    h4 v4 = {(f16)(dqacc[dt][4 * jq + 0] * p.smscale), (f16)(dqacc[dt][4 * jq + 1] * p.smscale),
+                             (f16)(dqacc[dt][4 * jq + 2] * p.smscale), (f16)(dqacc[dt][4 * jq + 3] * p.smscale)};
+                    *reinterpret_cast<h4 *>(dQr + d0) = v4;
+                } else {
+                    f32x4 v4 = {dqacc[dt][4 * jq + 0] * p.smscale, dqacc[dt][4 * jq + 1] * p.smscale,
+                                dqacc[dt][4 * jq + 2] * p.smscale, dqacc[dt][4 * jq + 3] * p.smscale};
+                    *reinterpret_cast<f32x4 *>(dQr + d0) = v4;
+                }
+            }
+        }
+}
+
+}  // namespace fpa

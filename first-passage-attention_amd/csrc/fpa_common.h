@@ -441,19 +441,26 @@ __device__ __forceinline__ void load_row_p1(OpRow<T, D> &dst, const T *rowp, boo
         p1_zero<T, D>(dst);
 }
 
+// Work-item and workgroup ids read from the hardware registers.  (Built with IEEE mode off,
+// the kernels cannot inline the device library's accessors behind threadIdx / blockIdx /
+// gridDim, which then become function calls.)
+__device__ __forceinline__ int thread_x() { return __builtin_amdgcn_workitem_id_x(); }
+__device__ __forceinline__ int group_x() { return __builtin_amdgcn_workgroup_id_x(); }
+__device__ __forceinline__ int group_y() { return __builtin_amdgcn_workgroup_id_y(); }
+
 // Work item of this workgroup in a grid of (ntiles, BH): rank 0 is the heaviest tile.
 // Workgroups are dispatched in linear order, round-robin over the 8 XCDs of the chip; when
 // BH is a multiple of 8 every head is pinned to one XCD (its K/V stay in that XCD's L2)
 // and each XCD takes its heads' tiles heaviest first.
-__device__ __forceinline__ void xcd_work_item(int &rank, int &bh, int BH) {
-    const int L = blockIdx.x + gridDim.x * blockIdx.y;
+__device__ __forceinline__ void xcd_work_item(int &rank, int &bh, int BH, int ntiles) {
+    const int L = group_x() + ntiles * group_y();
     if ((BH & 7) == 0) {
         const int xcd = L & 7, k = L >> 3, hpx = BH >> 3;
         rank = k / hpx;
         bh = (k % hpx) * 8 + xcd;
     } else {
-        rank = blockIdx.x;
-        bh = blockIdx.y;
+        rank = group_x();
+        bh = group_y();
     }
     rank = __builtin_amdgcn_readfirstlane(rank);  // uniform: loop bounds and addresses stay scalar
     bh = __builtin_amdgcn_readfirstlane(bh);

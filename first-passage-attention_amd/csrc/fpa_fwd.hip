@@ -30,9 +30,9 @@ namespace fpa {
 //   BSUF      : beta*log2e*SUF (the query side's per-key term)
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(64) fpa_stats_kernel(StatsParams p) {
-    const int blk = blockIdx.x, bh = blockIdx.y;
+    const int blk = group_x(), bh = group_y();
     const int b = bh / p.H, h = bh % p.H;
-    const int lane = threadIdx.x;
+    const int lane = thread_x();
     const int u = blk * G + lane;
     float ph = pinf(), ps = 0.f;
     if (u < p.T) {
@@ -117,11 +117,12 @@ fpa_fwd_kernel(FwdParams p) {
     // Per-key values of a tile: CA, CP, PHI and BST (the block's BMIN at [3][0]).
     __shared__ __attribute__((aligned(1024))) float cst[2][4][BN];
 
-    const int tid = threadIdx.x, lane = tid % 64, g = lane / 32, c = lane % 32;
+    const int tid = thread_x(), lane = tid % 64, g = lane / 32, c = lane % 32;
     const int w = __builtin_amdgcn_readfirstlane(tid / 64);  // wave index, uniform across the wave
+    const int nqt = (p.T + BM - 1) / BM;
     int rank, bh;
-    xcd_work_item(rank, bh, p.BH);
-    const int qt = gridDim.x - 1 - rank;  // longest rows first
+    xcd_work_item(rank, bh, p.BH, nqt);
+    const int qt = nqt - 1 - rank;  // longest rows first
     const int b = bh / p.H, h = bh % p.H;
     const int q0 = qt * BM, qw0 = q0 + 32 * w, tq = qw0 + c;
     const int ib = qw0 / G;

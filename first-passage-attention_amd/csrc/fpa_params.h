@@ -74,6 +74,7 @@ hipError_t launch_fwd(const FwdParams &p, int dtype, int D, hipStream_t s);
 hipError_t launch_bwd_prep(const BwdParams &p, int dtype, int D, hipStream_t s);
 hipError_t launch_bwd_kv(const BwdParams &p, int dtype, int D, hipStream_t s);
 hipError_t launch_bwd_q(const BwdParams &p, int dtype, int D, hipStream_t s);
+hipError_t launch_bwd_kvq(const BwdParams &p, int dtype, int D, hipStream_t s);  // both sides, one launch
 hipError_t launch_bwd_combine(const BwdParams &p, hipStream_t s);
 
 // Head dimensions with built kernels.

@@ -110,6 +110,31 @@ def test_kernel_deterministic(fpa):
         assert all(torch.equal(x, y) for x, y in zip(*runs))
 
 
+def test_fused_backward_matches_separate_launches(fpa):
+    """The backward's key and query sides run as one launch; launched one by one through the
+    phases bitmask they give bit-identical gradients (head counts with and without the per-XCD
+    head placement, a ragged T, and fp32 D128)."""
+    from fpa import _hip, _lib
+    dev = torch.device("cuda")
+    for (B, H, T, D, dtype), seed in (((2, 4, 600, 64, torch.float16), 14), ((1, 3, 333, 64, torch.float16), 15),
+                                      ((1, 2, 260, 128, torch.float32), 16), ((1, 2, 200, 64, torch.float32), 17)):
+        _say(f"[fused] B{B} H{H} T{T} D{D} {dtype}")
+        q, k, v, phi, psi, beta, do = (t.to(dev) for t in O.make_inputs(B, H, T, D, dtype=dtype, seed=seed))
+        fb = _hip.FwdBuffers(q)
+        _hip.run_fwd(_hip.fwd_args(q, k, v, phi, psi, beta, 1.0, fb), dev)
+        gb = _hip.BwdBuffers(q)
+        ba = _hip.bwd_args(q, k, v, beta, 1.0, fb, do, gb)
+        outs = []
+        for phases in ((0,), (_lib.FPA_BWD_DELTA, _lib.FPA_BWD_KEYS, _lib.FPA_BWD_QUERIES,
+                              _lib.FPA_BWD_PHI | _lib.FPA_BWD_BETA)):
+            for ph in phases:
+                ba.phases = ph
+                _hip.run_bwd(ba, dev)
+            torch.cuda.synchronize()
+            outs.append([t.clone() for t in (gb.dq, gb.dk, gb.dv, gb.dphi, gb.dpsi, gb.dbeta)])
+        assert all(torch.equal(x, y) for x, y in zip(*outs))
+
+
 def test_negative_and_zero_beta(fpa):
     """beta <= 0 flips / removes the bias; the kernels take the sign per head."""
     _say("[parity] beta = (-0.7, 0, 1.3)")
