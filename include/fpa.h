@@ -39,7 +39,8 @@ extern "C" {
 #define FPA_FWD_MAIN 2     /* the forward kernel (o, lse)                  */
 #define FPA_BWD_DELTA 1    /* Delta_t = sum_d dO o                         */
 #define FPA_BWD_KEYS 2     /* key side: dk, dv, dpsi, dbeta partials, ...  */
-#define FPA_BWD_QUERIES 4  /* query side: dq, query-block soft-min sums    */
+#define FPA_BWD_QUERIES 4  /* query side: dq, query-block soft-min sums;
+                              KEYS | QUERIES runs both sides as one kernel */
 #define FPA_BWD_PHI 8      /* dphi and dbeta (one kernel)                  */
 #define FPA_BWD_BETA 16    /* same kernel as FPA_BWD_PHI                   */
 
