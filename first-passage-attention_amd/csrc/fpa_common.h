@@ -320,24 +320,38 @@ template <typename T, int DT> struct Pad {
     template <int NR> static constexpr int bytes() { return NR * ROWB; }
 };
 
-// Raw buffer resource (SGPRs) over bytes [base, base + 2^31) of a wave-uniform pointer.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base) {
+// Raw buffer resource (four SGPRs) over bytes [base, base + 2^31) of a wave-uniform pointer:
+// base address (48 bits, stride 0), number of records, and the format word.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4 buf_rsrc(const void *base) {
     const uint64_t a = reinterpret_cast<uint64_t>(base);
-    const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
-    const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
-    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void *>((hi << 32) | lo), (short)0, 0x7fffffff,
-                                             0x00020000);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    return u32x4{lo, hi & 0xffffu, 0x7fffffffu, 0x00020000u};
 }
 
 // 16 bytes per lane from the buffer at byte offset voff straight into LDS at lds_dst + 16 * lane
-// (lds_dst wave-uniform).  Counted by vmcnt like a global load.
-__device__ __forceinline__ void buf_lds16(__amdgpu_buffer_rsrc_t r, uint32_t voff, void *lds_dst) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)(lds_dst), 16, voff, 0, 0, 0);
+// (lds_dst wave-uniform).  Counted by vmcnt like a global load.  Issued as inline assembly so that
+// the compiler does not track the LDS write: tracked, it makes every later LDS read it cannot
+// prove disjoint (the transposed reads among them) wait for all loads in flight, the next tile's
+// included.  The callers order these writes themselves: wait_loads() and a barrier before any
+// read of the tile.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t *)p);
+}
+__device__ __forceinline__ void buf_lds16(u32x4 r, uint32_t voff, void *lds_dst) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds_addr(lds_dst)), "v"(voff), "s"(r)
+                 : "m0");
 }
 
 // 4 bytes per lane (lds_dst + 4 * lane).
-__device__ __forceinline__ void buf_lds4(__amdgpu_buffer_rsrc_t r, uint32_t voff, void *lds_dst) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)(lds_dst), 4, voff, 0, 0, 0);
+__device__ __forceinline__ void buf_lds4(u32x4 r, uint32_t voff, void *lds_dst) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds_addr(lds_dst)), "v"(voff), "s"(r)
+                 : "m0");
 }
 
 // Wave-uniform element of memory that the running kernel does not write, read through the scalar
@@ -377,7 +391,7 @@ template <typename T, int D, int DT, int NR, int NW> struct TileLoader {
     // `tile`, through a buffer resource based at row row0 (the offsets stay 32-bit).
     __device__ __forceinline__ void issue(char *tile, const T *base, int64_t st, int row0, int T_, int wave,
                                           int lane) const {
-        const __amdgpu_buffer_rsrc_t rs = buf_rsrc(base + (int64_t)row0 * st);
+        const u32x4 rs = buf_rsrc(base + (int64_t)row0 * st);
         if (row0 + NR <= T_) {
 #pragma unroll
             for (int j = 0; j < PER; ++j) {
