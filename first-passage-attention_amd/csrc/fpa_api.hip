@@ -45,6 +45,34 @@ WsLayout ws_layout(int64_t B, int64_t H, int64_t T) {
 
 S3 s3(const int64_t *s) { return S3{s[0], s[1], s[2]}; }
 
+// Field scratch: the projection (or its gradient) as B * 3H * T floats, then the dW / dbias partials.
+struct FieldLayout {
+    int64_t lin, part, total;  // float offsets
+    int S;
+};
+FieldLayout field_layout(int64_t B, int64_t T, int64_t C, int64_t H) {
+    FieldLayout f;
+    const int64_t N = B * T;
+    f.S = (int)((N + 255) / 256 < 64 ? (N + 255) / 256 : 64);
+    f.lin = 0;
+    f.part = align64(B * 3 * H * T + 96);  // the dW kernel reads up to 96 floats past a position
+    f.total = f.part + align64((int64_t)f.S * 3 * H * (C + 1));  // the bias is feature C
+    return f;
+}
+
+int check_field(int64_t B, int64_t T, int64_t C, int64_t H, int32_t dtype, const void *x, const int64_t *sx,
+                const float *weight, const void *ws) {
+    if (B < 1 || T < 1 || C < 1 || H < 1) return fail(FPA_ERR_INVALID, "x must be (B, T, C) with B, T, C >= 1 and n_heads >= 1");
+    if (dtype != FPA_F16 && dtype != FPA_F32) return fail(FPA_ERR_INVALID, "x must be fp16 or fp32");
+    if (H > 32) return fail(FPA_ERR_UNSUPPORTED, "the Field kernels take at most 32 heads");
+    if (B > 65535 || B * T >= (int64_t(1) << 31) || C > (int64_t(1) << 24))
+        return fail(FPA_ERR_UNSUPPORTED, "x is too large for the Field kernels");
+    if (!x || !weight || !ws) return fail(FPA_ERR_INVALID, "x, weight and workspace must be non-NULL");
+    if (sx[0] < 0 || sx[1] < 0) return fail(FPA_ERR_INVALID, "x strides must be non-negative");
+    if ((reinterpret_cast<uintptr_t>(ws) & 255) != 0) return fail(FPA_ERR_INVALID, "workspace must be 256-byte aligned");
+    return FPA_OK;
+}
+
 // Shared checks of the forward and backward arguments.
 int check_common(int64_t B, int64_t H, int64_t T, int64_t D, int32_t dtype, float tau) {
     if (B < 1 || H < 1 || T < 1) return fail(FPA_ERR_INVALID, "q, k and v must have the same shape (B, H, T, D)");
@@ -80,7 +108,7 @@ int hip_fail(hipError_t e, const char *where) {
 
 extern "C" {
 
-int fpa_abi_version(void) { return 2; }
+int fpa_abi_version(void) { return 3; }
 
 const char *fpa_last_error(void) { return g_err.c_str(); }
 
@@ -95,6 +123,49 @@ int64_t fpa_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D, int3
     (void)D;
     (void)dtype;
     return ws_layout(B, H, T).total * (int64_t)sizeof(float);
+}
+
+int64_t fpa_field_workspace_bytes(int64_t B, int64_t T, int64_t C, int64_t H) {
+    return field_layout(B, T, C, H).total * (int64_t)sizeof(float);
+}
+
+int fpa_field_fwd(const FpaFieldFwdArgs *a, void *stream) {
+    g_err.clear();
+    if (a == nullptr) return fail(FPA_ERR_INVALID, "args is NULL");
+    int rc = check_field(a->B, a->T, a->C, a->H, a->dtype, a->x, a->sx, a->weight, a->workspace);
+    if (rc) return rc;
+    if (!a->bias || !a->phi || !a->psi) return fail(FPA_ERR_INVALID, "bias, phi and psi must be non-NULL");
+    const FieldLayout fl = field_layout(a->B, a->T, a->C, a->H);
+    FieldParams p = {};
+    p.x = a->x; p.sxb = a->sx[0]; p.sxt = a->sx[1];
+    p.w = a->weight; p.bias = a->bias;
+    p.lin = static_cast<float *>(a->workspace) + fl.lin;
+    p.phi = a->phi; p.psi = a->psi;
+    p.B = (int)a->B; p.T = (int)a->T; p.C = (int)a->C; p.H = (int)a->H; p.NO = 3 * (int)a->H; p.S = fl.S;
+    const hipError_t e = launch_field_fwd(p, a->dtype, reinterpret_cast<hipStream_t>(stream));
+    return e != hipSuccess ? hip_fail(e, "fpa_field_fwd launch") : FPA_OK;
+}
+
+int fpa_field_bwd(const FpaFieldBwdArgs *a, void *stream) {
+    g_err.clear();
+    if (a == nullptr) return fail(FPA_ERR_INVALID, "args is NULL");
+    int rc = check_field(a->B, a->T, a->C, a->H, a->dtype, a->x, a->sx, a->weight, a->workspace);
+    if (rc) return rc;
+    if (!a->dphi || !a->dpsi || !a->dweight || !a->dbias)
+        return fail(FPA_ERR_INVALID, "dphi, dpsi, dweight and dbias must be non-NULL");
+    if (a->dx && (a->sdx[0] < 0 || a->sdx[1] < 0)) return fail(FPA_ERR_INVALID, "dx strides must be non-negative");
+    const FieldLayout fl = field_layout(a->B, a->T, a->C, a->H);
+    FieldParams p = {};
+    p.x = a->x; p.sxb = a->sx[0]; p.sxt = a->sx[1];
+    p.dx = a->dx; p.sdxb = a->sdx[0]; p.sdxt = a->sdx[1];
+    p.w = a->weight;
+    p.lin = static_cast<float *>(a->workspace) + fl.lin;
+    p.part = static_cast<float *>(a->workspace) + fl.part;
+    p.dphi = a->dphi; p.dpsi = a->dpsi;
+    p.dw = a->dweight; p.dbias = a->dbias;
+    p.B = (int)a->B; p.T = (int)a->T; p.C = (int)a->C; p.H = (int)a->H; p.NO = 3 * (int)a->H; p.S = fl.S;
+    const hipError_t e = launch_field_bwd(p, a->dtype, reinterpret_cast<hipStream_t>(stream));
+    return e != hipSuccess ? hip_fail(e, "fpa_field_bwd launch") : FPA_OK;
 }
 
 int fpa_fwd(const FpaFwdArgs *a, void *stream) {

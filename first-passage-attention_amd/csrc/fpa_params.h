@@ -60,6 +60,20 @@ struct BwdParams {
     float il2;     // log2(e) / tau
 };
 
+// The Field prologue (projection of x to (delta, g, h), cumulative sum over t) and its gradient.
+struct FieldParams {
+    const void *x; int64_t sxb, sxt;    // (B, T, C), unit feature stride
+    void *dx; int64_t sdxb, sdxt;       // backward: x's dtype and layout rules (NULL: not computed)
+    const float *w;                     // (NO, C) row-major
+    const float *bias;                  // (NO,)
+    float *lin;                         // the projection (B, NO, T), or in the backward its gradient (B, T, NO)
+    float *phi, *psi;                   // (B, H, T) contiguous
+    const float *dphi, *dpsi;           // (B, H, T) contiguous
+    float *dw, *dbias;                  // (NO, C), (NO,)
+    float *part;                        // (S, NO, C + 1): dW and dbias partials over S splits of the B*T positions
+    int B, T, C, H, NO, S;              // NO = 3H
+};
+
 // BwdParams::qinfo holds, per 64-query block of a head, QI_PLANES planes of 64 floats
 // ([bh][block][plane][64]), so the key side stages a block's first four planes with one 1 KB load.
 // QI_BST holds the block's BMIN and BLSE at positions 0 and 1; planes 5-7 are unused.
@@ -76,6 +90,8 @@ hipError_t launch_bwd_kv(const BwdParams &p, int dtype, int D, hipStream_t s);
 hipError_t launch_bwd_q(const BwdParams &p, int dtype, int D, hipStream_t s);
 hipError_t launch_bwd_kvq(const BwdParams &p, int dtype, int D, hipStream_t s);  // both sides, one launch
 hipError_t launch_bwd_combine(const BwdParams &p, hipStream_t s);
+hipError_t launch_field_fwd(const FieldParams &p, int dtype, hipStream_t s);
+hipError_t launch_field_bwd(const FieldParams &p, int dtype, hipStream_t s);
 
 // Head dimensions with built kernels.
 inline bool supported_d(int dtype, int D) {

@@ -88,16 +88,39 @@ def _attention_packed(qkv, phi, psi, beta, tau, impl, block):
 
 class Field(nn.Module):
     """phi = W + g, psi = W + h with W = cumsum(delta), and beta = softplus(beta_raw), per head,
-    from x (B, T, d_model); delta, g and h are linear maps of x computed in fp32 (kernel.py:492-509)."""
+    from x (B, T, d_model); delta, g and h are linear maps of x computed in fp32 (kernel.py:492-509).
 
-    def __init__(self, d_model, n_heads, beta_init=1.0):
+    impl (not in the reference's signature; keyword only, default None): "hip" runs the projection
+    and the cumulative sum, and their gradient, on the HIP kernels (x fp16 or fp32 on the GPU, at
+    most 32 heads); "reference" runs them in PyTorch; None picks "hip" for GPU tensors it covers and
+    "reference" otherwise (float64 x, CPU tensors)."""
+
+    def __init__(self, d_model, n_heads, beta_init=1.0, *, impl=None):
         super().__init__()
         self.n_heads = n_heads
+        self.impl = impl
         self.proj = nn.Linear(d_model, 3 * n_heads)
         # inverse softplus, so that softplus(beta_raw) == beta_init
         self.beta_raw = nn.Parameter(torch.full((n_heads,), beta_init + math.log(-math.expm1(-beta_init))))
 
+    def _hip(self, x):
+        covered = x.is_cuda and x.dtype in (torch.float16, torch.float32) and x.dim() == 3 and self.n_heads <= 32
+        if self.impl is None:
+            return covered
+        if self.impl in _HIP_NAMES:
+            if not covered:
+                raise ValueError("Field with impl='hip' needs x (B, T, C) fp16 or fp32 on a ROCm GPU "
+                                 "and at most 32 heads")
+            return True
+        if self.impl != "reference":
+            raise ValueError(f"unknown implementation {self.impl!r}")
+        return False
+
     def forward(self, x):
+        if self._hip(x):
+            from ._hip import FieldHIP  # loads libfpa.so; raises if it is missing
+            phi, psi = FieldHIP.apply(x, self.proj.weight, self.proj.bias, self.n_heads)
+            return phi, psi, F.softplus(self.beta_raw)
         B, T, _ = x.shape
         dt = torch.float64 if x.dtype == torch.float64 else torch.float32
         with torch.autocast(device_type=x.device.type, enabled=False):
@@ -119,7 +142,7 @@ class FirstPassageAttention(nn.Module):
         self.tau, self.impl, self.block = tau, impl, block
         self.qkv = nn.Linear(d_model, 3 * d_model, bias=False)
         self.out = nn.Linear(d_model, d_model, bias=False)
-        self.field = Field(d_model, n_heads, beta_init)
+        self.field = Field(d_model, n_heads, beta_init, impl=impl)
 
     def forward(self, x):
         B, T, _ = x.shape

@@ -169,3 +169,61 @@ class FirstPassageAttentionPackedHIP(torch.autograd.Function):
             grads = BwdBuffers(q, dqkv=dqkv)
             run_bwd(bwd_args(q, k, v, beta, ctx.tau, _Saved(o, lse, state), do, grads), dev)
         return dqkv, grads.dphi, grads.dpsi, grads.dbeta, None
+
+
+class FieldHIP(torch.autograd.Function):
+    """Field's projection and cumulative sum (kernel.py:502-509) on the HIP kernels:
+    x (B, T, C) fp16 or fp32 -> phi, psi (B, H, T) fp32, computed in fp32 like the reference.
+    The backward gives dx (x's dtype), d(weight) and d(bias) in a fixed summation order."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, n_heads):
+        B, T, C = x.shape
+        if x.stride(2) != 1:
+            x = x.contiguous()
+        w = weight.float().contiguous()
+        b = bias.float().contiguous()
+        L = _lib.lib()
+        dev = x.device
+        with torch.cuda.device(dev):
+            phi = torch.empty((B, n_heads, T), dtype=torch.float32, device=dev)
+            psi = torch.empty_like(phi)
+            ws = torch.empty(L.fpa_field_workspace_bytes(B, T, C, n_heads), dtype=torch.uint8, device=dev)
+            a = _lib.FpaFieldFwdArgs()
+            a.B, a.T, a.C, a.H = B, T, C, n_heads
+            a.dtype = _lib.dtype_code(x.dtype)
+            a.x, a.sx = _lib.ptr(x), (x.stride(0), x.stride(1))
+            a.weight, a.bias = _lib.ptr(w), _lib.ptr(b)
+            a.phi, a.psi, a.workspace = _lib.ptr(phi), _lib.ptr(psi), _lib.ptr(ws)
+            _lib.check(L.fpa_field_fwd(a, _lib.stream_of(dev)))
+        ctx.save_for_backward(x, w, ws)
+        ctx.n_heads = n_heads
+        ctx.wdtype, ctx.bdtype = weight.dtype, bias.dtype
+        return phi, psi
+
+    @staticmethod
+    def backward(ctx, dphi, dpsi):
+        x, w, ws = ctx.saved_tensors
+        B, T, C = x.shape
+        H = ctx.n_heads
+        dev = x.device
+        zeros = None
+        if dphi is None or dpsi is None:
+            zeros = torch.zeros((B, H, T), dtype=torch.float32, device=dev)
+        dphi = zeros if dphi is None else dphi.float().contiguous()
+        dpsi = zeros if dpsi is None else dpsi.float().contiguous()
+        L = _lib.lib()
+        with torch.cuda.device(dev):
+            dx = torch.empty_like(x) if ctx.needs_input_grad[0] else None
+            dw = torch.empty_like(w)
+            db = torch.empty(w.shape[0], dtype=torch.float32, device=dev)
+            a = _lib.FpaFieldBwdArgs()
+            a.B, a.T, a.C, a.H = B, T, C, H
+            a.dtype = _lib.dtype_code(x.dtype)
+            a.x, a.sx = _lib.ptr(x), (x.stride(0), x.stride(1))
+            a.weight, a.dphi, a.dpsi = _lib.ptr(w), _lib.ptr(dphi), _lib.ptr(dpsi)
+            a.dx = _lib.ptr(dx) if dx is not None else None
+            a.sdx = (dx.stride(0), dx.stride(1)) if dx is not None else (0, 0)
+            a.dweight, a.dbias, a.workspace = _lib.ptr(dw), _lib.ptr(db), _lib.ptr(ws)
+            _lib.check(L.fpa_field_bwd(a, _lib.stream_of(dev)))
+        return dx, dw.to(ctx.wdtype), db.to(ctx.bdtype), None

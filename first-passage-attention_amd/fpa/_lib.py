@@ -9,7 +9,7 @@ import os
 
 import torch
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libfpa.so")
 
 FPA_F16, FPA_F32 = 0, 1
@@ -43,6 +43,21 @@ class FpaBwdArgs(ctypes.Structure):
                 ("phases", ctypes.c_int32)]
 
 
+_S2 = _i64 * 2
+
+
+class FpaFieldFwdArgs(ctypes.Structure):
+    _fields_ = [("B", _i64), ("T", _i64), ("C", _i64), ("H", _i64), ("dtype", ctypes.c_int32),
+                ("x", _vp), ("sx", _S2), ("weight", _vp), ("bias", _vp), ("phi", _vp), ("psi", _vp),
+                ("workspace", _vp)]
+
+
+class FpaFieldBwdArgs(ctypes.Structure):
+    _fields_ = [("B", _i64), ("T", _i64), ("C", _i64), ("H", _i64), ("dtype", ctypes.c_int32),
+                ("x", _vp), ("sx", _S2), ("weight", _vp), ("dphi", _vp), ("dpsi", _vp),
+                ("dx", _vp), ("sdx", _S2), ("dweight", _vp), ("dbias", _vp), ("workspace", _vp)]
+
+
 class FpaError(RuntimeError):
     """A failed libfpa call (status code and message of fpa_last_error)."""
 
@@ -74,6 +89,12 @@ def lib():
     L.fpa_fwd.argtypes = [ctypes.POINTER(FpaFwdArgs), _vp]
     L.fpa_bwd.restype = ctypes.c_int
     L.fpa_bwd.argtypes = [ctypes.POINTER(FpaBwdArgs), _vp]
+    L.fpa_field_workspace_bytes.restype = _i64
+    L.fpa_field_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64]
+    L.fpa_field_fwd.restype = ctypes.c_int
+    L.fpa_field_fwd.argtypes = [ctypes.POINTER(FpaFieldFwdArgs), _vp]
+    L.fpa_field_bwd.restype = ctypes.c_int
+    L.fpa_field_bwd.argtypes = [ctypes.POINTER(FpaFieldBwdArgs), _vp]
     if L.fpa_abi_version() != ABI_VERSION:
         raise RuntimeError(f"libfpa.so ABI {L.fpa_abi_version()} != {ABI_VERSION}: rebuild it")
     _LIB = L

@@ -16,7 +16,11 @@
  *               (165-370) and the dbeta sum at kernel.py:450 (four kernels here:
  *               delta, key side, query side, phi/beta combine);
  *   fpa_state_floats / fpa_bwd_workspace_bytes <- the scratch allocations of
- *               kernel.py:390-392, 406-407, 430-436, sized so the caller owns them.
+ *               kernel.py:390-392, 406-407, 430-436, sized so the caller owns them;
+ *   fpa_field_fwd <- Field.forward (kernel.py:502-509): the fp32 projection of x
+ *               to (delta, g, h), W = cumsum_t delta, phi = W + g, psi = W + h;
+ *   fpa_field_bwd <- the autograd backward of those operations (dx, dW, dbias
+ *               from dphi, dpsi), which the reference leaves to torch.
  * Error behaviour mirrors the validation of first_passage_attention
  * (kernel.py:467-486): invalid shapes or dtypes return FPA_ERR_INVALID with the
  * reference's message available from fpa_last_error().
@@ -101,6 +105,44 @@ typedef struct {
                         for per-kernel timing only: a partial run reads the workspace
                         left by an earlier full run and leaves skipped outputs unwritten. */
 } FpaBwdArgs;
+
+/* Field prologue of the layer (kernel.py:492-509).  x is (B, T, C) with a unit feature stride,
+ * fp16 or fp32; the projection (3H outputs, H <= 32) is computed in fp32. */
+typedef struct {
+    int64_t B, T, C, H;
+    int32_t dtype;          /* of x: FPA_F16 or FPA_F32 */
+    const void *x;
+    int64_t sx[2];          /* element strides of b and t */
+    const float *weight;    /* (3H, C) row-major: Field.proj.weight */
+    const float *bias;      /* (3H,): Field.proj.bias */
+    float *phi;             /* (B, H, T) contiguous */
+    float *psi;             /* (B, H, T) contiguous */
+    void *workspace;        /* fpa_field_workspace_bytes(), 256-byte aligned */
+} FpaFieldFwdArgs;
+
+typedef struct {
+    int64_t B, T, C, H;
+    int32_t dtype;          /* of x and dx */
+    const void *x;
+    int64_t sx[2];
+    const float *weight;    /* (3H, C) */
+    const float *dphi;      /* (B, H, T) contiguous */
+    const float *dpsi;      /* (B, H, T) contiguous */
+    void *dx;               /* (B, T, C) like x, or NULL to skip it */
+    int64_t sdx[2];
+    float *dweight;         /* (3H, C) */
+    float *dbias;           /* (3H,) */
+    void *workspace;        /* fpa_field_workspace_bytes(), 256-byte aligned */
+} FpaFieldBwdArgs;
+
+/* Bytes of scratch of fpa_field_fwd and fpa_field_bwd (the larger of the two). */
+int64_t fpa_field_workspace_bytes(int64_t B, int64_t T, int64_t C, int64_t H);
+
+/* Enqueue the Field forward (phi, psi) on `stream`. */
+int fpa_field_fwd(const FpaFieldFwdArgs *args, void *stream);
+
+/* Enqueue the Field backward (dx, dweight, dbias) on `stream`.  Deterministic. */
+int fpa_field_bwd(const FpaFieldBwdArgs *args, void *stream);
 
 /* Floats of the forward state (block statistics) for a (B, H, T) problem. */
 int64_t fpa_state_floats(int64_t B, int64_t H, int64_t T);

@@ -20,6 +20,10 @@ What it restates (reference ``kernel.py`` of yliu-fort/first-passage-attention):
   gradient at equality.
 * ``kernel.py:57-64`` -- causal softmax attention with autocast off.
 
+* ``kernel.py:502-509`` -- the layer's Field: ``(delta, g, h) = x W^T + b`` in fp32
+  (float64 for float64 x), ``W = cumsum_t delta``, ``phi = W + g``, ``psi = W + h``
+  (:func:`field_phi_psi`; :func:`field_by_loops` restates it with loops for tiny shapes).
+
 Two independent formulations live here so that tests can pin one with the
 other: :func:`fpa_forward` / :func:`fpa_grads` (dense tensors + autograd, the
 reference's own formulation) and :func:`explicit_grads` (closed-form gradient
@@ -215,6 +219,35 @@ def make_inputs(B, H, T, D, dtype=torch.float16, seed=0, phi_scale=1.0, ties=Fal
         raise ValueError(beta)
     do = torch.randn(B, H, T, D, generator=g).to(dtype)
     return q, k, v, phi, psi, b, do
+
+
+def field_phi_psi(x, weight, bias, n_heads):
+    """phi, psi (B, H, T) of Field.forward (kernel.py:502-509) in float64, differentiable in x,
+    weight and bias: lin = x W^T + b viewed as (B, T, 3, H) = (delta, g, h); W = cumsum_t delta."""
+    B, T, _ = x.shape
+    lin = x.double() @ weight.double().T + bias.double()
+    d, g, h = lin.view(B, T, 3, n_heads).permute(2, 0, 3, 1)
+    w = d.cumsum(-1)
+    return w + g, w + h
+
+
+def field_by_loops(x, weight, bias, n_heads):
+    """field_phi_psi with explicit loops (tiny shapes only): output o = j * H + h of the
+    projection is delta (j = 0), g (j = 1) or h (j = 2) of head h."""
+    x, weight, bias = (np.asarray(a.detach().double()) for a in (x, weight, bias))
+    B, T, C = x.shape
+    phi = np.zeros((B, n_heads, T))
+    psi = np.zeros((B, n_heads, T))
+    for b in range(B):
+        for hh in range(n_heads):
+            run = 0.0
+            for t in range(T):
+                lin = [sum(x[b, t, c] * weight[j * n_heads + hh, c] for c in range(C)) + bias[j * n_heads + hh]
+                       for j in range(3)]
+                run += lin[0]
+                phi[b, hh, t] = run + lin[1]
+                psi[b, hh, t] = run + lin[2]
+    return torch.from_numpy(phi), torch.from_numpy(psi)
 
 
 def rel_err(x, ref):

@@ -42,7 +42,8 @@ def test_struct_layout_matches_header(tmp_path):
     if cc is None:
         pytest.skip("no C compiler")
     lines = []
-    for cls, cname in ((_lib.FpaFwdArgs, "FpaFwdArgs"), (_lib.FpaBwdArgs, "FpaBwdArgs")):
+    for cls, cname in ((_lib.FpaFwdArgs, "FpaFwdArgs"), (_lib.FpaBwdArgs, "FpaBwdArgs"),
+                       (_lib.FpaFieldFwdArgs, "FpaFieldFwdArgs"), (_lib.FpaFieldBwdArgs, "FpaFieldBwdArgs")):
         lines.append(f'printf("{cname} sizeof %zu\\n", sizeof({cname}));')
         for n, _ in cls._fields_:
             lines.append(f'printf("{cname} {n} %zu\\n", offsetof({cname}, {n}));')
@@ -198,3 +199,37 @@ def test_field_matches_definition():
     d, g, h = lin.view(2, 9, 3, 2).permute(2, 0, 3, 1)
     assert torch.allclose(phi, d.cumsum(-1) + g, atol=1e-5)
     assert torch.allclose(psi, d.cumsum(-1) + h, atol=1e-5)
+
+
+def _field_args(**kw):
+    a = _lib.FpaFieldFwdArgs()
+    a.B, a.T, a.C, a.H, a.dtype = 2, 100, 48, 4, _lib.FPA_F32
+    a.x, a.sx = 4096, (4800, 48)
+    a.weight, a.bias, a.phi, a.psi, a.workspace = 8192, 8192, 8192, 8192, 1 << 20
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("field,value,code,msg", [
+    ("B", 0, _lib.FPA_ERR_INVALID, "B, T, C >= 1"),
+    ("H", 33, _lib.FPA_ERR_UNSUPPORTED, "at most 32 heads"),
+    ("dtype", 7, _lib.FPA_ERR_INVALID, "fp16 or fp32"),
+    ("x", None, _lib.FPA_ERR_INVALID, "non-NULL"),
+    ("workspace", (1 << 20) + 64, _lib.FPA_ERR_INVALID, "256-byte aligned"),
+])
+def test_field_c_abi_validation(field, value, code, msg):
+    """fpa_field_fwd rejects bad arguments before any launch (no GPU needed)."""
+    L = _lib.lib()
+    rc = L.fpa_field_fwd(_field_args(**{field: value}), None)
+    assert rc == code
+    assert msg in L.fpa_last_error().decode()
+
+
+def test_field_workspace_size():
+    """The projection as B*3H*T floats plus the dW / dbias partials (at most 64 splits of the positions)."""
+    L = _lib.lib()
+    B, T, C, H = 8, 2048, 768, 12
+    S = min(64, (B * T + 255) // 256)
+    up = lambda n: (n + 63) // 64 * 64
+    assert L.fpa_field_workspace_bytes(B, T, C, H) == 4 * (up(B * 3 * H * T + 96) + up(S * 3 * H * (C + 1)))

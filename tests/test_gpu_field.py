@@ -1,0 +1,122 @@
+"""The layer's Field prologue on the HIP kernels (fpa_field_fwd / fpa_field_bwd) against the
+float64 definition of kernel.py:502-509 (oracle.field_phi_psi) and its autograd gradient.
+
+Tolerances: phi, psi, dW, dbias and fp32 dx within 1e-5 of the largest reference value (fp32
+accumulation over C features and T positions); fp16 dx within 2e-3 (its rounding).
+"""
+import pytest
+import torch
+
+import fpa
+from oracle import fpa_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def hip():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    from fpa import _hip, _lib
+    _lib.lib()
+    return _hip
+
+
+def _rel(x, r):
+    return ((x.double().cpu() - r).abs().max() / r.abs().max().clamp(min=1e-30)).item()
+
+
+def _case(hip, x, H, seed):
+    """(phi, psi, dx, dW, db) from the HIP kernels and from the float64 definition."""
+    g = torch.Generator().manual_seed(seed)
+    B, T, C = x.shape
+    w = torch.randn(3 * H, C, generator=g) / C ** 0.5
+    b = torch.randn(3 * H, generator=g)
+    dphi, dpsi = torch.randn(B, H, T, generator=g), torch.randn(B, H, T, generator=g)
+    dev = "cuda"
+    xd = x.to(dev).requires_grad_()
+    wd, bd = w.to(dev).requires_grad_(), b.to(dev).requires_grad_()
+    phi, psi = hip.FieldHIP.apply(xd, wd, bd, H)
+    dx, dw, db = torch.autograd.grad((phi, psi), (xd, wd, bd), (dphi.to(dev), dpsi.to(dev)))
+    xr = x.detach().double().requires_grad_()
+    wr, br = w.double().requires_grad_(), b.double().requires_grad_()
+    rphi, rpsi = O.field_phi_psi(xr, wr, br, H)
+    rdx, rdw, rdb = torch.autograd.grad((rphi, rpsi), (xr, wr, br), (dphi.double(), dpsi.double()))
+    return (phi, psi, dx, dw, db), (rphi.detach(), rpsi.detach(), rdx, rdw, rdb)
+
+
+@pytest.mark.parametrize("B,T,C,H,dtype", [
+    (2, 100, 48, 4, torch.float32),
+    (1, 1, 16, 1, torch.float32),
+    (3, 257, 70, 5, torch.float32),
+    (2, 300, 96, 12, torch.float16),
+    (1, 64, 768, 32, torch.float32),
+])
+def test_field_matches_the_definition(hip, B, T, C, H, dtype):
+    _say(f"[field] B{B} T{T} C{C} H{H} {dtype}")
+    x = torch.randn(B, T, C, generator=torch.Generator().manual_seed(B * 1000 + T)).to(dtype)
+    got, ref = _case(hip, x, H, seed=T + C)
+    for name, a, r in zip(("phi", "psi", "dx", "dW", "dbias"), got, ref):
+        assert a.dtype == (dtype if name == "dx" else torch.float32), name
+        assert torch.isfinite(a).all(), name
+        tol = 2e-3 if (name == "dx" and dtype == torch.float16) else 1e-5
+        assert _rel(a, r) <= tol, (name, _rel(a, r))
+
+
+def test_field_strided_x_and_determinism(hip):
+    """x as a view with a row stride wider than C (the features of a larger tensor), and two runs
+    bit-identical."""
+    _say("[field] strided x, determinism")
+    base = torch.randn(2, 130, 80, generator=torch.Generator().manual_seed(9))
+    x = base[:, :, 8:72]
+    assert x.stride() == (130 * 80, 80, 1)
+    got, ref = _case(hip, x, 3, seed=10)
+    for name, a, r in zip(("phi", "psi", "dx", "dW", "dbias"), got, ref):
+        assert _rel(a, r) <= 1e-5, (name, _rel(a, r))
+    again, _ = _case(hip, x, 3, seed=10)
+    assert all(torch.equal(a, b) for a, b in zip(got, again))
+
+
+def test_field_lm_shape_against_fp32_torch(hip):
+    """The cfg5 LM shape (B8 T2048 C768 H12, fp32 x): phi, psi and the gradients against the
+    reference's own fp32 formulation on the GPU."""
+    _say("[field] B8 T2048 C768 H12 fp32 against torch fp32")
+    dev = "cuda"
+    g = torch.Generator().manual_seed(11)
+    B, T, C, H = 8, 2048, 768, 12
+    x = torch.randn(B, T, C, generator=g).to(dev).requires_grad_()
+    f = fpa.Field(C, H, impl="hip").to(dev)
+    r = fpa.Field(C, H, impl="reference").to(dev)
+    r.load_state_dict(f.state_dict())
+    dphi, dpsi = torch.randn(B, H, T, generator=g).to(dev), torch.randn(B, H, T, generator=g).to(dev)
+    outs = []
+    for m in (f, r):
+        phi, psi, _ = m(x)
+        grads = torch.autograd.grad((phi, psi), (x, m.proj.weight, m.proj.bias), (dphi, dpsi))
+        outs.append([phi.detach(), psi.detach()] + [t.detach() for t in grads])
+    for name, a, b in zip(("phi", "psi", "dx", "dW", "dbias"), *outs):
+        err = ((a - b).abs().max() / b.abs().max()).item()
+        assert err <= 1e-4, (name, err)
+
+
+def test_layer_uses_the_field_kernels(hip):
+    """The layer on the GPU with impl=None runs Field through the kernels and matches the
+    reference layer (fp32)."""
+    _say("[field] layer impl=None vs reference")
+    torch.manual_seed(12)
+    dev = "cuda"
+    m = fpa.FirstPassageAttention(64, 4).to(dev)
+    r = fpa.FirstPassageAttention(64, 4, impl="reference").to(dev)
+    r.load_state_dict(m.state_dict())
+    assert m.field._hip(torch.empty(1, 1, 64, device=dev))
+    x = torch.randn(2, 90, 64, device=dev)
+    ya, yb = m(x), r(x)
+    ga = torch.autograd.grad(ya.sum(), list(m.parameters()))
+    gb = torch.autograd.grad(yb.sum(), list(r.parameters()))
+    assert ((ya - yb).norm() / yb.norm()).item() <= 1e-4
+    for a, b in zip(ga, gb):
+        assert ((a - b).norm() / b.norm().clamp(min=1e-30)).item() <= 1e-4

@@ -119,3 +119,31 @@ def test_tau_must_be_positive():
     phi, psi, beta = random_field(1, 1, 4, seed=0)
     with pytest.raises(ValueError, match="tau must be positive"):
         O.first_passage_bias(phi, psi, beta, tau=0.0)
+
+
+def test_field_oracle_is_the_loop_definition():
+    """field_phi_psi (tensor form) against field_by_loops (projection and running sum by hand)."""
+    g = torch.Generator().manual_seed(3)
+    x, w, b = torch.randn(2, 7, 5, generator=g), torch.randn(9, 5, generator=g), torch.randn(9, generator=g)
+    phi, psi = O.field_phi_psi(x, w, b, 3)
+    lphi, lpsi = O.field_by_loops(x, w, b, 3)
+    assert torch.allclose(phi, lphi, rtol=1e-12, atol=1e-12)
+    assert torch.allclose(psi, lpsi, rtol=1e-12, atol=1e-12)
+
+
+def test_field_oracle_special_cases():
+    """With zero weights phi and psi are t * bias_delta + bias_g / bias_h; with a single position
+    there is no sum, phi = delta + g."""
+    x = torch.randn(1, 6, 4)
+    w = torch.zeros(6, 4)
+    b = torch.tensor([1.0, -2.0, 0.5, 3.0, 0.25, -1.0])  # delta (h0, h1), g (h0, h1), h (h0, h1)
+    phi, psi = O.field_phi_psi(x, w, b, 2)
+    t = torch.arange(1, 7, dtype=torch.float64)
+    assert torch.allclose(phi[0, 0], 1.0 * t + 0.5) and torch.allclose(phi[0, 1], -2.0 * t + 3.0)
+    assert torch.allclose(psi[0, 0], 1.0 * t + 0.25) and torch.allclose(psi[0, 1], -2.0 * t - 1.0)
+    x1 = torch.randn(1, 1, 4, dtype=torch.float64)
+    w1 = torch.randn(3, 4, dtype=torch.float64)
+    b1 = torch.randn(3, dtype=torch.float64)
+    p1, s1 = O.field_phi_psi(x1, w1, b1, 1)
+    lin = x1[0, 0] @ w1.T + b1
+    assert torch.allclose(p1[0, 0, 0], lin[0] + lin[1]) and torch.allclose(s1[0, 0, 0], lin[0] + lin[2])
