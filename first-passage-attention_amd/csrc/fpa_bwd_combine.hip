@@ -16,7 +16,11 @@
 // Z(u) = Z(u-1) 2^{m(u-1) - m(u)} + 2^{a_u - m(u)}, and the reverse chain
 // lam(u) = g_us + rho(u) lam(u+1) with rho(u) = Z(u) 2^{m(u) - m(u+1)} / Z(u+1) gives the
 // contribution 2^{a_u - m(u)} lam(u) / Z(u) to u.  Only FMAs sit on the dependent chains,
-// and the 64 steps are split over the four waves of the workgroup.
+// and the 64 steps are split over the four waves of the workgroup.  When a spans at most
+// INBLOCK_SPREAD binades over the block, one reference (the block maximum c_U) serves every
+// column instead: Z(u) 2^{-c_U} is a running sum of positive terms 2^{a_v - c_U}, and the
+// contribution to u is 2^{a_u - c_U} sum_{t>=u} g_ts 2^{c_U} / Z(t) (one reciprocal per pair
+// instead of the chains' exponentials).
 //
 // dbeta[h] is summed (fixed order) by the workgroup of block 0 of batch 0 of head h.
 // All sums run in a fixed order: the result is bit-reproducible.
@@ -24,6 +28,9 @@
 #include "fpa_params.h"
 
 namespace fpa {
+
+// Largest spread of a over a block (binades) for the single-reference in-block sums.
+constexpr float INBLOCK_SPREAD = 100.f;
 
 // Maximum over an array of n values held in LDS, scanned by one wave: out[i] = max of in[i..hi)
 // (suffix) or of in(lo..i] (prefix), with elements outside [lo, hi) treated as -inf.  Each lane
@@ -147,11 +154,50 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
         SU = block_sum_256(acc, red, w, lane);
     }
 
+    // Spread of a over the block (cU is its maximum): a single reference for the in-block soft-min
+    // sums when it is small.
+    float amin = (lane <= last) ? sA[lane] : pinf();
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) amin = fminf(amin, __shfl_xor(amin, o, 64));
+    if (cU - amin <= INBLOCK_SPREAD) {
+        // Every term of Z relative to 2^{c_U}: e_v = 2^{a_v - c_U} >= 2^-INBLOCK_SPREAD, so the running
+        // sums Z'(u) = sum_{s<v<=u} e_v are sums of positive terms that cannot underflow, and the
+        // contribution to u of column s is e_u sum_{t>=u} g_ts / Z'(t).  Lane s owns column s,
+        // wave w the steps u in [16w, 16w + 16); segment sums are joined through LDS.
+        const int s = lane, u0 = 16 * w;
+        float ev[16], Zs = 0.f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int u = u0 + k;
+            ev[k] = (u > s && u <= last) ? fexp2(sA[u] - cU) : 0.f;
+            Zs += ev[k];
+        }
+        segZ[w][s] = Zs;
+        __syncthreads();
+        float Z = 0.f;
+        for (int v = 0; v < w; ++v) Z += segZ[v][s];  // the sum entering this segment
+        float qv[16], Qs = 0.f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            Z += ev[k];
+            qv[k] = (ev[k] > 0.f) ? gq[k / 4][k % 4] * frcp(Z) : 0.f;
+            Qs += qv[k];
+        }
+        segA[w][s] = Qs;
+        __syncthreads();
+        float rev = 0.f;
+        for (int v = 3; v > w; --v) rev += segA[v][s];  // sum of g / Z' beyond this segment
+#pragma unroll
+        for (int k = 15; k >= 0; --k) {
+            rev += qv[k];
+            contrib[u0 + k][s] = ev[k] * rev;
+        }
+    } else {
     // In-block pairs.  Lane s owns column s; wave w owns the steps u in [16w, 16w + 16).
     // Each wave runs its segment of both chains locally, the segments are joined through LDS
     // (forward states combine associatively, reverse affine maps compose), and each wave then
-    // reruns its segment from the joined state.
-    {
+    // reruns its segment from the joined state.  Running maxima keep every term representable
+    // whatever the spread of a.
         const int s = lane, u0 = 16 * w;
         float m = ninf(), Z = 0.f;
 #pragma unroll
