@@ -20,7 +20,8 @@
 // INBLOCK_SPREAD binades over the block, one reference (the block maximum c_U) serves every
 // column instead: Z(u) 2^{-c_U} is a running sum of positive terms 2^{a_v - c_U}, and the
 // contribution to u is 2^{a_u - c_U} sum_{t>=u} g_ts 2^{c_U} / Z(t) (one reciprocal per pair
-// instead of the chains' exponentials).
+// instead of the chains' exponentials), and the key-block and query-block parts become sums of
+// per-position terms 2^{c_U - C_s} W_s and 2^{c_U - c_t} R_t times 2^{a_u - c_U}.
 //
 // dbeta[h] is summed (fixed order) by the workgroup of block 0 of batch 0 of head h.
 // All sums run in a fixed order: the result is bit-reproducible.
@@ -87,6 +88,7 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
     __shared__ float sA[G], sC[G], sc[G], sW[G], sR[G];
     __shared__ float segM[4][G], segZ[4][G], segM2[4][G], segZ2[4][G], segA[4][G], segB[4][G], pp[4][G];
     __shared__ float contrib[G][G + 1];      // [u][s]
+    __shared__ float sF[G], sH[G];           // single-reference key-block and query-block terms
     __shared__ float red[4];
 
     const int U = group_x(), bh = group_y(), b = bh / p.H, h = bh % p.H;
@@ -159,12 +161,18 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
     float amin = (lane <= last) ? sA[lane] : pinf();
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) amin = fminf(amin, __shfl_xor(amin, o, 64));
-    if (cU - amin <= INBLOCK_SPREAD) {
+    const bool fast = cU - amin <= INBLOCK_SPREAD;  // uniform over the workgroup
+    if (fast) {
         // Every term of Z relative to 2^{c_U}: e_v = 2^{a_v - c_U} >= 2^-INBLOCK_SPREAD, so the running
         // sums Z'(u) = sum_{s<v<=u} e_v are sums of positive terms that cannot underflow, and the
         // contribution to u of column s is e_u sum_{t>=u} g_ts / Z'(t).  Lane s owns column s,
         // wave w the steps u in [16w, 16w + 16); segment sums are joined through LDS.
         const int s = lane, u0 = 16 * w;
+        if (w == 0) {  // key-block and query-block terms relative to c_U (C_s, c_t <= c_U)
+            const bool vs = s <= last;
+            sF[s] = (vs && sC[s] > ninf()) ? fexp2(cU - sC[s]) * sW[s] : 0.f;
+            sH[s] = vs ? fexp2(cU - sc[s]) * sR[s] : 0.f;
+        }
         float ev[16], Zs = 0.f;
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
@@ -279,14 +287,27 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
         float part = 0.f, p4 = 0.f;
         if (u <= last) {
             const float au = sA[u];
+            if (fast) {  // 2^{a_u - c_U} (sum_{v<u} sF[v] + sum_{v>=u} sH[v])
 #pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                const int v = v0 + k;
-                if (v < u) {
-                    part = fmaf(fexp2(au - sC[v]), sW[v], part);
-                    p4 += contrib[u][v];
+                for (int k = 0; k < 16; ++k) {
+                    const int v = v0 + k;
+                    if (v < u) {
+                        part += sF[v];
+                        p4 += contrib[u][v];
+                    }
+                    if (v >= u && v <= last) part += sH[v];
                 }
-                if (v >= u && v <= last) part = fmaf(fexp2(au - sc[v]), sR[v], part);
+                part *= fexp2(au - cU);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 16; ++k) {
+                    const int v = v0 + k;
+                    if (v < u) {
+                        part = fmaf(fexp2(au - sC[v]), sW[v], part);
+                        p4 += contrib[u][v];
+                    }
+                    if (v >= u && v <= last) part = fmaf(fexp2(au - sc[v]), sR[v], part);
+                }
             }
         }
         pp[w][u] = part + p4;
