@@ -158,9 +158,7 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
 
     // Spread of a over the block (cU is its maximum): a single reference for the in-block soft-min
     // sums when it is small.
-    float amin = (lane <= last) ? sA[lane] : pinf();
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) amin = fminf(amin, __shfl_xor(amin, o, 64));
+    const float amin = wave_min((lane <= last) ? sA[lane] : pinf());
     const bool fast = cU - amin <= INBLOCK_SPREAD;  // uniform over the workgroup
     if (fast) {
         // Every term of Z relative to 2^{c_U}: e_v = 2^{a_v - c_U} >= 2^-INBLOCK_SPREAD, so the running

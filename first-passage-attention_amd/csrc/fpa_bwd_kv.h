@@ -34,7 +34,7 @@ namespace fpa {
 //   LQ    -lse_t / sc2 (-inf past T) and DL = -Delta_t (0 past T), Delta_t = sum_d dO_td O_td: the
 //         start values of the S and dP accumulators, so the MFMA chains subtract them for free;
 //         rows past T get -inf scores and P = 0 with no per-element mask
-//   BPRE  beff * PRE_t (beff = beta * log2e, or 2^-100 for beta = 0; +-inf past T)
+//   PRE   PRE_t, the running minimum of phi from the start of t's block (+inf past T)
 //   ZQ    with PRL_t = PREL_t - BLSE <= 0 (BLSE = log2 sum 2^a over t's block; 0 past T):
 //         2^{PRL_t} > 0 when the block's spread -PRL_{first row} is at most PROD_SPREAD
 //         (product form of the soft-min denominators), else PRL_t <= 0 (exact form).  The sign
@@ -52,7 +52,7 @@ struct KvShared {
     static constexpr int TB = Pad<T, (D < 32 ? 32 : D)>::template bytes<64>();  // one padded Q or dO tile
     __attribute__((aligned(1024))) char Qs[2][TB];
     __attribute__((aligned(1024))) char dOs[2][TB];
-    __attribute__((aligned(1024))) float qi[2][5][64];  // per-query values of a block: LQ, DL, BPRE, ZQ, BST
+    __attribute__((aligned(1024))) float qi[2][5][64];  // per-query values of a block: LQ, DL, PRE, ZQ, BST
     __attribute__((aligned(16))) float kPHI[32 * NW];
 };
 
@@ -82,7 +82,7 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
     const T *Kb = static_cast<const T *>(p.k) + b * p.sk.b + h * p.sk.h;
     const T *Vb = static_cast<const T *>(p.v) + b * p.sv.b + h * p.sv.h;
     const T *DOb = static_cast<const T *>(p.dout) + b * p.sdo.b + h * p.sdo.h;
-    // A block's per-query values: planes 0-3 (LQ, DL, BPRE, ZQ) with one 1 KB load, BST with a 256 B one.
+    // A block's per-query values: planes 0-3 (LQ, DL, PRE, ZQ) with one 1 KB load, BST with a 256 B one.
     const float *qi_head = p.qinfo + qi_at(bh, p.NB, 0, 0);
 
     TileLoader<T, D, DT, BQ, NW> qld, dld;
@@ -103,8 +103,10 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
     load_row_p1<T, D>(vreg, Vb + (int64_t)s * p.sv.t, s_valid, g);
 
     // Bias terms scaled by beff = beta * log2e (2^-100 for beta = 0, below fp32 resolution in the
-    // exponent): v = beff * x with x = min(SUF_s, MID, PRE_t) - psi_s, bm = beff * min(x, 0) =
-    // med3(v, 0, E), and the gate x <= 0 is bm == v for either sign of beta.
+    // exponent).  Off the diagonal, x = min(SUF_s, MID, PRE_t) - psi_s splits into a per-key part
+    // and a per-query part: bm = beff * min(x, 0) = med3(beff PRE_t - beff psi_s, cAz, E) with
+    // cAz = beff * min(SUF_s - psi_s, MID - psi_s, 0), and the gate x <= 0 is PRE_t <= thr with
+    // thr = +inf when min(SUF_s, MID) <= psi_s (every query passes), else psi_s.
     const float beta = p.beta[h], beff = beta_eff(beta * LOG2E);
     const float E = (beff > 0.f) ? ninf() : pinf();  // med3(x, y, E) = min (beff > 0) or max
     float psi_s = 0.f, suf = pinf(), sufl = ninf();
@@ -139,9 +141,10 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
     float mid = pinf(), midl = ninf(), cmid = ninf();  // over blocks strictly between jb and ib
     const float *phiblk = kPHI + (sb - k0);
 
-    // Block statistics used by a query block, loaded one block ahead: BMIN / BLSE of block
-    // ib - 1 (which joins the middle) and BLSE of block ib.
-    float bm_prev = 0.f, bl_prev = 0.f;  // block ib - 1, from the previous block's staged values
+    // The soft-min reference rs = max(C_s, cmid) and sv = 2^{SUFL_s - rs} + 2^{MIDL - rs} of the
+    // current query block.  After a block the middle takes in its BMIN / BLSE (staged with the
+    // block's per-query values) and both are recomputed for the next block, before its barrier.
+    float rs = Cs, sv = (Cs > ninf()) ? fexp2(sufl - Cs) : 0.f;
     wait_loads();
     __syncthreads();
     for (int ib = ib0, it = 0; ib < p.NB; ++ib, ++it) {
@@ -156,24 +159,19 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
             // one FMA per element instead of an exp2.  The clamp only changes terms whose
             // 2^{PREL_t - rs} exceeds 2^{126 - PROD_SPREAD}, where 1/Z is already below 2^{-26} of
             // the other terms.
-            float rs = ninf(), rsb = ninf(), sv = 0.f, ck = 0.f;
+            float rsb = ninf(), ck = 0.f;
             bool prod = false;
             if (ib > jb) {
-                if (ib - 1 > jb) {  // block ib - 1 joins the middle
-                    mid = fminf(mid, bm_prev);
-                    midl = lse2_pair(midl, bl_prev);
-                    cmid = fmaxf(cmid, -bm_prev * p.il2);
-                }
-                rs = fmaxf(Cs, cmid);
-                sv = (rs > ninf()) ? fexp2(sufl - rs) + fexp2(midl - rs) : 0.f;
                 rsb = rs - bl_cur;
                 ck = fexp2(fminf(-rsb, 126.f));
                 prod = uniform_f(qi[buf][QI_ZQ][0]) > 0.f;
             }
-            const float cA = __builtin_amdgcn_fmed3f(bsuf, beff * mid, E);  // beff * min(SUF_s, MID)
+            const float cAz = __builtin_amdgcn_fmed3f(__builtin_amdgcn_fmed3f(bsuf, beff * mid, E) - bpsi, 0.f, E);
+            const float thr = (fminf(suf, mid) <= psi_s) ? pinf() : psi_s;
+            const float nbpsi = -bpsi;
             const char *Qt = Qs[buf];
             const char *Dt = dOs[buf];
-            const float *rBPRE = qi[buf][QI_BPRE];
+            const float *rPRE = qi[buf][QI_PRE];
             const bool diag = (ib == jb);
             const int sr = s - sb;
             float r = pinf();  // running min of phi over (s, u] for the in-block scan
@@ -195,16 +193,15 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
 #pragma unroll
                         for (int jq = 0; jq < 4; ++jq) {
                             const int t4 = 32 * mt + 8 * jq + 4 * g;
-                            const f32x4 bpre4 = *reinterpret_cast<const f32x4 *>(&rBPRE[t4]);
+                            const f32x4 pre4 = *reinterpret_cast<const f32x4 *>(&rPRE[t4]);
                             const f32x4 zq4 = *reinterpret_cast<const f32x4 *>(&rZQ[t4]);
 #pragma unroll
                             for (int e = 0; e < 4; ++e) {
                                 const int j = 4 * jq + e;
-                                const float v = __builtin_amdgcn_fmed3f(cA, bpre4[e], E) - bpsi;
-                                const float bm = __builtin_amdgcn_fmed3f(v, 0.f, E);
+                                const float bm = __builtin_amdgcn_fmed3f(fmaf(pre4[e], beff, nbpsi), cAz, E);
                                 const float P = fexp2(fmaf(S[j], p.sc2, bm));
                                 const float dS = P * dP[j];
-                                const float gg = (bm == v) ? dS : 0.f;
+                                const float gg = (pre4[e] <= thr) ? dS : 0.f;
                                 gsum += gg;
                                 dbacc = fmaf(dS, bm, dbacc);
                                 const float z = PROD ? fmaf(zq4[e], ck, sv) : sv + fexp2(zq4[e] - rsb);
@@ -258,8 +255,13 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
                 }
             }
         }
-        bm_prev = bm_here;
-        bl_prev = bl_cur;
+        if (wave_active && ib > jb) {  // block ib joins the middle of the blocks after it
+            mid = fminf(mid, bm_here);
+            midl = lse2_pair(midl, bl_cur);
+            cmid = fmaxf(cmid, -bm_here * p.il2);
+            rs = fmaxf(Cs, cmid);
+            sv = (rs > ninf()) ? fexp2(sufl - rs) + fexp2(midl - rs) : 0.f;
+        }
         wait_loads();
         __syncthreads();
     }

@@ -480,11 +480,30 @@ __device__ __forceinline__ void xcd_work_item(int &rank, int &bh, int BH, int nt
     bh = __builtin_amdgcn_readfirstlane(bh);
 }
 
-// Sum over the 64 lanes of a wave, fixed order (butterfly).
+// Lane exchange within rows of 16 lanes by a DPP pattern (every source lane is inside the row).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+// Reduction over the 64 lanes of a wave in a fixed order, result in every lane: lanes ^1 and ^2
+// (quad_perm), the quads and halves of each 16-lane row (row_half_mirror, row_mirror), then rows
+// 0+1 / 2+3 (permlane16 swap) and the two 32-lane halves (permlane32 swap).  VALU only, no LDS.
+template <typename Op>
+__device__ __forceinline__ float wave_reduce(float x, Op op) {
+    x = op(x, dpp_f<0xB1>(x));   // quad_perm [1,0,3,2]
+    x = op(x, dpp_f<0x4E>(x));   // quad_perm [2,3,0,1]
+    x = op(x, dpp_f<0x141>(x));  // row_half_mirror
+    x = op(x, dpp_f<0x140>(x));  // row_mirror
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return op(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
 __device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o, 64);
-    return x;
+    return wave_reduce(x, [](float a, float b) { return a + b; });
+}
+__device__ __forceinline__ float wave_min(float x) {
+    return wave_reduce(x, [](float a, float b) { return fminf(a, b); });
 }
 
 
