@@ -52,7 +52,7 @@ struct KvShared {
     static constexpr int TB = Pad<T, (D < 32 ? 32 : D)>::template bytes<64>();  // one padded Q or dO tile
     __attribute__((aligned(1024))) char Qs[2][TB];
     __attribute__((aligned(1024))) char dOs[2][TB];
-    __attribute__((aligned(1024))) float qi[2][5][64];  // per-query values of a block: LQ, DL, PRE, ZQ, BST
+    __attribute__((aligned(1024))) float qi[2][QI_PLANES][64];  // per-query values of a block: LQ, DL, PRE, ZQ, BST
     __attribute__((aligned(16))) float kPHI[32 * NW];
 };
 
@@ -82,7 +82,9 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
     const T *Kb = static_cast<const T *>(p.k) + b * p.sk.b + h * p.sk.h;
     const T *Vb = static_cast<const T *>(p.v) + b * p.sv.b + h * p.sv.h;
     const T *DOb = static_cast<const T *>(p.dout) + b * p.sdo.b + h * p.sdo.h;
-    // A block's per-query values: planes 0-3 (LQ, DL, PRE, ZQ) with one 1 KB load, BST with a 256 B one.
+    // A block's per-query values: planes 0-3 (LQ, DL, PRE, ZQ) and 4-7 (BST, three unused) with one
+    // 1 KB load each, from the even and the odd waves (no wave-dependent branch).  After the last
+    // block the prefetch repeats it into the other buffer, which is not read again.
     const float *qi_head = p.qinfo + qi_at(bh, p.NB, 0, 0);
 
     TileLoader<T, D, DT, BQ, NW> qld, dld;
@@ -91,9 +93,9 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
     auto issue = [&](int ib, int buf) {
         qld.issue(Qs[buf], Qb, p.sq.t, ib * BQ, p.T, w, lane);
         dld.issue(dOs[buf], DOb, p.sdo.t, ib * BQ, p.T, w, lane);
-        if (w == NW - 1) buf_lds16(buf_rsrc(qi_head + (int64_t)ib * QI_PLANES * 64), 16 * lane, &qi[buf][0][0]);
-        if (w == (NW >= 2 ? NW - 2 : 0))
-            buf_lds4(buf_rsrc(qi_head + (int64_t)ib * QI_PLANES * 64), 4 * (QI_BST * 64 + lane), &qi[buf][4][0]);
+#pragma unroll
+        for (int hq = (NW >= 2 ? w % 2 : 0); hq < 2; hq += (NW >= 2 ? 2 : 1))
+            buf_lds16(buf_rsrc(qi_head + (int64_t)ib * QI_PLANES * 64), 1024 * hq + 16 * lane, &qi[buf][4 * hq][0]);
     };
     const int ib0 = k0 / G;
     issue(ib0, 0);
@@ -149,7 +151,7 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
     __syncthreads();
     for (int ib = ib0, it = 0; ib < p.NB; ++ib, ++it) {
         const int buf = it & 1;
-        if (ib + 1 < p.NB) issue(ib + 1, buf ^ 1);
+        issue(umin_i(ib + 1, p.NB - 1), buf ^ 1);
         const float bm_here = qi[buf][QI_BST][0], bl_cur = qi[buf][QI_BST][1];  // block ib
         if (wave_active && ib >= jb) {
             // Soft-min denominators off the diagonal: Z_ts 2^{-rs} = sv + 2^{PREL_t - rs} with the

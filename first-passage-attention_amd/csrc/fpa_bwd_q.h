@@ -39,8 +39,9 @@ struct QShared {
     __attribute__((aligned(1024))) char Ks[2][TB];
     __attribute__((aligned(1024))) char Vs[2][TB];
     // Per-key values of a block: BSUF, CP (= betal * psi), SUFL, PHI, and BST (BMIN, BLSE, SUF of the
-    // first key at [4][0..2]).
-    __attribute__((aligned(1024))) float kst[2][5][64];
+    // first key at [4][0..2]; planes 4-7 are four copies, so the two halves are one 1 KB load each
+    // from the even and the odd waves).
+    __attribute__((aligned(1024))) float kst[2][8][64];
     __attribute__((aligned(16))) float Aw[NW][64];  // per-wave key factors of the shared-reference path
 };
 
@@ -74,7 +75,7 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
     const int kpl = (lane < 16) ? PL_BSUF : (lane < 32) ? PL_CP : (lane < 48) ? PL_SUFL : PL_PHI;
     const float *st_head = p.state + L.at(0, bh, 0);
     const uint32_t kst_off = (uint32_t)((kpl * p.TP + 4 * (lane & 15)) * 4);  // bytes from plane 0 of the head
-    const uint32_t bst_off = (uint32_t)((PL_BST * p.TP + lane) * 4);
+    const uint32_t bst_off = (uint32_t)((PL_BST * p.TP + 4 * (lane & 15)) * 4);  // four copies of BST
 
     TileLoader<T, D, DT, BK, NW> kld, vld;
     kld.init(p.sk.t, w, lane);
@@ -82,8 +83,9 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
     auto issue = [&](int jb, int buf) {
         kld.issue(Ks[buf], Kb, p.sk.t, jb * BK, p.T, w, lane);
         vld.issue(Vs[buf], Vb, p.sv.t, jb * BK, p.T, w, lane);
-        if (w == NW - 1) buf_lds16(buf_rsrc(st_head + jb * BK), kst_off, &kst[buf][0][0]);
-        if (w == (NW >= 2 ? NW - 2 : 0)) buf_lds4(buf_rsrc(st_head + jb * BK), bst_off, &kst[buf][4][0]);
+#pragma unroll
+        for (int hq = (NW >= 2 ? w % 2 : 0); hq < 2; hq += (NW >= 2 ? 2 : 1))
+            buf_lds16(buf_rsrc(st_head + jb * BK), hq ? bst_off : kst_off, &kst[buf][4 * hq][0]);
     };
     const int jbmax = umin_i(p.NB - 1, (q0 + BM - 1) / BK);
     issue(jbmax, 0);
@@ -130,7 +132,7 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
     for (int jb = jbmax, it = 0; jb >= 0; --jb, ++it) {
         const int buf = it & 1;
         const int s0 = jb * BK;
-        if (jb > 0) issue(jb - 1, buf ^ 1);
+        issue(jb > 0 ? jb - 1 : 0, buf ^ 1);
         const float bm_here = kst[buf][4][0], bl_here = kst[buf][4][1], suf_first = kst[buf][4][2];
         if (wave_active && jb <= ib) {
             const float *kSUF = kst[buf][0], *kPSI = kst[buf][1], *kSUFL = kst[buf][2], *kPHI = kst[buf][3];

@@ -364,8 +364,10 @@ __device__ __forceinline__ void wait_loads() { asm volatile("s_waitcnt vmcnt(0)"
 
 // Loads NR-row tiles of one (B, H, T, D)-strided tensor (d stride 1, rows 16-byte aligned,
 // 64 * row stride < 2^31 bytes) into padded LDS tiles.  The NI wave instructions of a tile
-// are shared out over the NW waves of the workgroup; each wave keeps the byte offsets of its
-// lanes' source chunks relative to the tile's first row, so a full tile costs no VALU work.
+// are shared out over the NW waves of the workgroup (when NW does not divide NI, the waves past
+// the last instruction issue it again: identical writes instead of a wave-dependent branch); each
+// wave keeps the byte offsets of its lanes' source chunks relative to the tile's first row, so a
+// full tile costs no VALU work.
 template <typename T, int D, int DT, int NR, int NW> struct TileLoader {
     using P = Pad<T, DT>;
     static constexpr int CPRD = D / P::CE;                // chunks of data in a row
@@ -383,7 +385,7 @@ template <typename T, int D, int DT, int NR, int NW> struct TileLoader {
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
             int r, lc;
-            slot(wave + NW * j, lane, r, lc);
+            slot(min(wave + NW * j, NI - 1), lane, r, lc);
             off[j] = (uint32_t)((r * st + lc * P::CE) * (int64_t)sizeof(T));
         }
     }
@@ -395,19 +397,17 @@ template <typename T, int D, int DT, int NR, int NW> struct TileLoader {
         if (row0 + NR <= T_) {
 #pragma unroll
             for (int j = 0; j < PER; ++j) {
-                const int i = wave + NW * j;
-                if (NI % NW == 0 || i < NI) buf_lds16(rs, off[j], tile + 1024 * i);
+                const int i = min(wave + NW * j, NI - 1);  // waves past the last instruction repeat it
+                buf_lds16(rs, off[j], tile + 1024 * i);
             }
         } else {
             const int rmax = T_ - 1 - row0;  // rows past T read row T - 1
 #pragma unroll
             for (int j = 0; j < PER; ++j) {
-                const int i = wave + NW * j;
-                if (NI % NW == 0 || i < NI) {
-                    int r, lc;
-                    slot(i, lane, r, lc);
-                    buf_lds16(rs, (uint32_t)((min(r, rmax) * st + lc * P::CE) * (int64_t)sizeof(T)), tile + 1024 * i);
-                }
+                const int i = min(wave + NW * j, NI - 1);
+                int r, lc;
+                slot(i, lane, r, lc);
+                buf_lds16(rs, (uint32_t)((min(r, rmax) * st + lc * P::CE) * (int64_t)sizeof(T)), tile + 1024 * i);
             }
         }
     }

@@ -138,14 +138,16 @@ fpa_fwd_kernel(FwdParams p) {
     const float *st_head = p.state + L.at(0, bh, 0);
     const uint32_t cst_off = (uint32_t)((((lane < 16) ? PL_CA : (lane < 32) ? PL_CP : (lane < 48) ? PL_PHI : PL_BST) * p.TP + 4 * (lane & 15)) * 4);
 
-    // Tile jt of K, V and the per-key values into buffer `buf` (shared out over the waves).
+    // Tile jt of K, V and the per-key values into buffer `buf` (shared out over the waves; every wave
+    // issues the per-key load, identical writes instead of a wave-dependent branch).  After tile 0
+    // the prefetch repeats it into the other buffer, which is not read again.
     TileLoader<T, D, DT, BN, NW> kld, vld;
     kld.init(p.sk.t, w, lane);
     vld.init(p.sv.t, w, lane);
     auto issue = [&](int jt, int buf) {
         kld.issue(Ks[buf], Kb, p.sk.t, jt * BN, p.T, w, lane);
         vld.issue(Vs[buf], Vb, p.sv.t, jt * BN, p.T, w, lane);
-        if (w == NW - 1) buf_lds16(buf_rsrc(st_head + jt * BN), cst_off, &cst[buf][0][0]);
+        buf_lds16(buf_rsrc(st_head + jt * BN), cst_off, &cst[buf][0][0]);
     };
 
     const int nkt = (p.T + BN - 1) / BN;
@@ -170,7 +172,7 @@ fpa_fwd_kernel(FwdParams p) {
     for (int jt = jtmax, it = 0; jt >= 0; --jt, ++it) {
         const int buf = it & 1;
         const int s0 = jt * BN;
-        if (jt > 0) issue(jt - 1, buf ^ 1);
+        issue(jt > 0 ? jt - 1 : 0, buf ^ 1);
         if (wave_active && s0 <= qw0 + 31) {
             const char *Kt = Ks[buf];
             const float *cA = cst[buf][0], *cP = cst[buf][1], *cPHI = cst[buf][2];
