@@ -90,12 +90,13 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
     TileLoader<T, D, DT, BQ, NW> qld, dld;
     qld.init(p.sq.t, w, lane);
     dld.init(p.sdo.t, w, lane);
+    const uint32_t aQ = lds_addr(&Qs[0][0]), aD = lds_addr(&dOs[0][0]), aI = lds_addr(&qi[0][0][0]);
     auto issue = [&](int ib, int buf) {
-        qld.issue(Qs[buf], Qb, p.sq.t, ib * BQ, p.T, w, lane);
-        dld.issue(dOs[buf], DOb, p.sdo.t, ib * BQ, p.T, w, lane);
+        qld.issue(aQ + buf * sizeof(Qs[0]), Qb, p.sq.t, ib * BQ, p.T, w, lane);
+        dld.issue(aD + buf * sizeof(dOs[0]), DOb, p.sdo.t, ib * BQ, p.T, w, lane);
 #pragma unroll
         for (int hq = (NW >= 2 ? w % 2 : 0); hq < 2; hq += (NW >= 2 ? 2 : 1))
-            buf_lds16(buf_rsrc(qi_head + (int64_t)ib * QI_PLANES * 64), 1024 * hq + 16 * lane, &qi[buf][4 * hq][0]);
+            buf_lds16(buf_rsrc(qi_head + (int64_t)ib * QI_PLANES * 64), 1024 * hq + 16 * lane, aI + buf * sizeof(qi[0]) + 1024 * hq);
     };
     const int ib0 = k0 / G;
     issue(ib0, 0);

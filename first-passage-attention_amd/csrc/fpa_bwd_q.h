@@ -80,12 +80,13 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
     TileLoader<T, D, DT, BK, NW> kld, vld;
     kld.init(p.sk.t, w, lane);
     vld.init(p.sv.t, w, lane);
+    const uint32_t aK = lds_addr(&Ks[0][0]), aV = lds_addr(&Vs[0][0]), aS = lds_addr(&kst[0][0][0]);
     auto issue = [&](int jb, int buf) {
-        kld.issue(Ks[buf], Kb, p.sk.t, jb * BK, p.T, w, lane);
-        vld.issue(Vs[buf], Vb, p.sv.t, jb * BK, p.T, w, lane);
+        kld.issue(aK + buf * sizeof(Ks[0]), Kb, p.sk.t, jb * BK, p.T, w, lane);
+        vld.issue(aV + buf * sizeof(Vs[0]), Vb, p.sv.t, jb * BK, p.T, w, lane);
 #pragma unroll
         for (int hq = (NW >= 2 ? w % 2 : 0); hq < 2; hq += (NW >= 2 ? 2 : 1))
-            buf_lds16(buf_rsrc(st_head + jb * BK), hq ? bst_off : kst_off, &kst[buf][4 * hq][0]);
+            buf_lds16(buf_rsrc(st_head + jb * BK), hq ? bst_off : kst_off, aS + buf * sizeof(kst[0]) + 1024 * hq);
     };
     const int jbmax = umin_i(p.NB - 1, (q0 + BM - 1) / BK);
     issue(jbmax, 0);

@@ -331,7 +331,9 @@ __device__ __forceinline__ u32x4 buf_rsrc(const void *base) {
 }
 
 // 16 bytes per lane from the buffer at byte offset voff straight into LDS at lds_dst + 16 * lane
-// (lds_dst wave-uniform).  Counted by vmcnt like a global load.  Issued as inline assembly so that
+// (lds_dst a wave-uniform LDS byte address; the kernels take lds_addr of each staging array once
+// and add constant offsets, since every conversion of a generic pointer to an LDS address costs a
+// null check on the scalar unit).  Counted by vmcnt like a global load.  Issued as inline assembly so that
 // the compiler does not track the LDS write: tracked, it makes every later LDS read it cannot
 // prove disjoint (the transposed reads among them) wait for all loads in flight, the next tile's
 // included.  The callers order these writes themselves: wait_loads() and a barrier before any
@@ -339,18 +341,18 @@ __device__ __forceinline__ u32x4 buf_rsrc(const void *base) {
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t *)p);
 }
-__device__ __forceinline__ void buf_lds16(u32x4 r, uint32_t voff, void *lds_dst) {
+__device__ __forceinline__ void buf_lds16(u32x4 r, uint32_t voff, uint32_t lds_dst) {
     asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                  :
-                 : "s"(lds_addr(lds_dst)), "v"(voff), "s"(r)
+                 : "s"(lds_dst), "v"(voff), "s"(r)
                  : "m0");
 }
 
 // 4 bytes per lane (lds_dst + 4 * lane).
-__device__ __forceinline__ void buf_lds4(u32x4 r, uint32_t voff, void *lds_dst) {
+__device__ __forceinline__ void buf_lds4(u32x4 r, uint32_t voff, uint32_t lds_dst) {
     asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
                  :
-                 : "s"(lds_addr(lds_dst)), "v"(voff), "s"(r)
+                 : "s"(lds_dst), "v"(voff), "s"(r)
                  : "m0");
 }
 
@@ -391,7 +393,7 @@ template <typename T, int D, int DT, int NR, int NW> struct TileLoader {
     }
     // Rows row0 .. row0 + NR - 1 (wave-uniform row0 < T_) of the tensor whose row 0 is `base` into
     // `tile`, through a buffer resource based at row row0 (the offsets stay 32-bit).
-    __device__ __forceinline__ void issue(char *tile, const T *base, int64_t st, int row0, int T_, int wave,
+    __device__ __forceinline__ void issue(uint32_t tile, const T *base, int64_t st, int row0, int T_, int wave,
                                           int lane) const {
         const u32x4 rs = buf_rsrc(base + (int64_t)row0 * st);
         if (row0 + NR <= T_) {

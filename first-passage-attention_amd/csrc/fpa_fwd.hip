@@ -144,10 +144,11 @@ fpa_fwd_kernel(FwdParams p) {
     TileLoader<T, D, DT, BN, NW> kld, vld;
     kld.init(p.sk.t, w, lane);
     vld.init(p.sv.t, w, lane);
+    const uint32_t aK = lds_addr(&Ks[0][0]), aV = lds_addr(&Vs[0][0]), aC = lds_addr(&cst[0][0][0]);
     auto issue = [&](int jt, int buf) {
-        kld.issue(Ks[buf], Kb, p.sk.t, jt * BN, p.T, w, lane);
-        vld.issue(Vs[buf], Vb, p.sv.t, jt * BN, p.T, w, lane);
-        buf_lds16(buf_rsrc(st_head + jt * BN), cst_off, &cst[buf][0][0]);
+        kld.issue(aK + buf * sizeof(Ks[0]), Kb, p.sk.t, jt * BN, p.T, w, lane);
+        vld.issue(aV + buf * sizeof(Vs[0]), Vb, p.sv.t, jt * BN, p.T, w, lane);
+        buf_lds16(buf_rsrc(st_head + jt * BN), cst_off, aC + buf * sizeof(cst[0]));
     };
 
     const int nkt = (p.T + BN - 1) / BN;
