@@ -13,9 +13,14 @@
 #include "fpa_common.h"
 #include "fpa_params.h"
 
-// Tuning knob (build-time): waves per SIMD of the D <= 64 forward kernel.
+// Tuning knobs (build-time): waves per SIMD of the D <= 64 forward kernel, fp16 and fp32.  Three
+// fp16 waves fit in 168 VGPRs each; with 3 workgroups per CU the cfg2 grid (768 workgroups) is
+// resident at once.  The fp32 D = 64 kernel needs about 200 VGPRs.
 #ifndef FPA_FWD_WPE
-#define FPA_FWD_WPE 2
+#define FPA_FWD_WPE 3
+#endif
+#ifndef FPA_FWD_WPE32
+#define FPA_FWD_WPE32 2
 #endif
 
 namespace fpa {
@@ -304,7 +309,7 @@ fpa_fwd_kernel(FwdParams p) {
 
 template <typename T, int D>
 static hipError_t launch_fwd_t(const FwdParams &p, hipStream_t s) {
-    constexpr int NW = FPA_NW, WPE = (D >= 128) ? 1 : FPA_FWD_WPE;
+    constexpr int NW = FPA_NW, WPE = (D >= 128) ? 1 : (sizeof(T) == 2 ? FPA_FWD_WPE : FPA_FWD_WPE32);
     const int nqt = (p.T + 32 * NW - 1) / (32 * NW);
     hipLaunchKernelGGL((fpa_fwd_kernel<T, D, WPE, NW>), dim3(nqt, p.BH), dim3(64 * NW), 0, s, p);
     return hipGetLastError();
