@@ -27,6 +27,13 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-I", os.path.
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
+# The backward tiles hold about 240 VGPRs at two waves per SIMD; LLVM's iterative ILP scheduling
+# strategy orders their block loops for more overlap than the default occupancy-driven one
+# (3% on the fused backward at cfg2, same register budget, no spills).
+PER_FILE = {f: ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"]
+            for f in ("fpa_bwd_fused.hip", "fpa_bwd_kv.hip", "fpa_bwd_q.hip")}
+
+
 def hipcc():
     cand = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not os.path.exists(cand):
@@ -36,7 +43,7 @@ def hipcc():
 
 def _compile(src):
     obj = os.path.join(BUILD, os.path.basename(src).replace(".hip", ".o"))
-    cmd = [hipcc()] + COMMON + ["-c", src, "-o", obj]
+    cmd = [hipcc()] + COMMON + PER_FILE.get(os.path.basename(src), []) + ["-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stdout}\n{r.stderr}")
