@@ -178,7 +178,8 @@ def main():
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(FPA shards over batch and heads with no communication; see DESIGN.md)", file=sys.stderr)
+              "(FPA shards over batch and heads with no communication, so one GPU's share is the "
+              "same kernel at B/n or H/n)", file=sys.stderr)
         sys.exit(2)
 
     if a.workload == "lm":
