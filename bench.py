@@ -50,7 +50,6 @@ CONFIGS = {
 
 def make_inputs(cfg, seed=0):
     import torch
-    from oracle import fpa_oracle  # noqa: F401  (only for the cpu_baseline leg; inputs are built here)
     dt = torch.float16 if cfg["dtype"] == "f16" else torch.float32
     B, H, T, D = cfg["B"], cfg["H"], cfg["T"], cfg["D"]
     g = torch.Generator().manual_seed(seed)

@@ -41,9 +41,17 @@ def hipcc():
     return cand
 
 
-def _compile(src):
+def _srchash():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("fpa_srchash", os.path.join(HERE, "fpa", "_srchash.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod.source_hash()
+
+
+def _compile(src, defs=()):
     obj = os.path.join(BUILD, os.path.basename(src).replace(".hip", ".o"))
-    cmd = [hipcc()] + COMMON + PER_FILE.get(os.path.basename(src), []) + ["-c", src, "-o", obj]
+    cmd = [hipcc()] + COMMON + list(defs) + PER_FILE.get(os.path.basename(src), []) + ["-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stdout}\n{r.stderr}")
@@ -54,8 +62,11 @@ def build(verbose=True):
     os.makedirs(BUILD, exist_ok=True)
     srcs = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
     workers = min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
+    # The source hash goes into fpa_api.hip only (fpa_source_hash()); the loader compares it.
+    defs = {s: ([f'-DFPA_SOURCE_HASH="{_srchash()}"'] if os.path.basename(s) == "fpa_api.hip" else [])
+            for s in srcs}
     with concurrent.futures.ThreadPoolExecutor(workers) as ex:
-        objs = list(ex.map(_compile, srcs))
+        objs = list(ex.map(lambda s: _compile(s, defs[s]), srcs))
     tmp = OUT + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs
     r = subprocess.run(cmd, capture_output=True, text=True)

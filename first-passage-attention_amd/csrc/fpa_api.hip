@@ -106,9 +106,15 @@ int hip_fail(hipError_t e, const char *where) {
 
 }  // namespace
 
+#ifndef FPA_SOURCE_HASH
+#define FPA_SOURCE_HASH "unknown"
+#endif
+
 extern "C" {
 
 int fpa_abi_version(void) { return 3; }
+
+const char *fpa_source_hash(void) { return FPA_SOURCE_HASH; }
 
 const char *fpa_last_error(void) { return g_err.c_str(); }
 

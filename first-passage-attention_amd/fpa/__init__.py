@@ -49,6 +49,12 @@ def _check_hip(q, k, v, phi, psi, beta, tau, impl, block):
         raise ValueError("tau must be positive")
     if not q.is_cuda:
         raise RuntimeError("impl='hip' needs q, k, v on a ROCm GPU")
+    # The kernels dereference every pointer on q's device: a tensor elsewhere (a CPU beta, say)
+    # is refused here, before any launch.
+    for name, t in (("k", k), ("v", v), ("phi", phi), ("psi", psi), ("beta", beta)):
+        if t.device != q.device:
+            raise ValueError(f"{name} is on {t.device}, but q is on {q.device}: impl='hip' needs every "
+                             "tensor on the same GPU")
     return beta
 
 
@@ -92,28 +98,30 @@ class Field(nn.Module):
 
     impl (not in the reference's signature; keyword only, default None): "hip" runs the projection
     and the cumulative sum, and their gradient, on the HIP kernels (x fp16 or fp32 on the GPU, at
-    most 32 heads); "reference" runs them in PyTorch; None picks "hip" for GPU tensors it covers and
-    "reference" otherwise (float64 x, CPU tensors)."""
+    most 32 heads) and raises for inputs outside that; "reference" runs them in PyTorch; None picks
+    "hip" for GPU tensors it covers and "reference" otherwise (float64 x, CPU tensors, more than
+    32 heads)."""
 
     def __init__(self, d_model, n_heads, beta_init=1.0, *, impl=None):
         super().__init__()
         self.n_heads = n_heads
+        if impl is not None and impl not in _HIP_NAMES and impl != "reference":
+            raise ValueError(f"unknown implementation {impl!r}")
         self.impl = impl
         self.proj = nn.Linear(d_model, 3 * n_heads)
         # inverse softplus, so that softplus(beta_raw) == beta_init
         self.beta_raw = nn.Parameter(torch.full((n_heads,), beta_init + math.log(-math.expm1(-beta_init))))
 
     def _hip(self, x):
-        covered = x.is_cuda and x.dtype in (torch.float16, torch.float32) and x.dim() == 3 and self.n_heads <= 32
+        covered = (x.is_cuda and x.dtype in (torch.float16, torch.float32) and x.dim() == 3
+                   and self.n_heads <= 32 and self.proj.weight.device == x.device)
         if self.impl is None:
             return covered
         if self.impl in _HIP_NAMES:
             if not covered:
-                raise ValueError("Field with impl='hip' needs x (B, T, C) fp16 or fp32 on a ROCm GPU "
-                                 "and at most 32 heads")
+                raise ValueError("Field with impl='hip' needs x (B, T, C) fp16 or fp32 and its weights on one "
+                                 "ROCm GPU, and at most 32 heads")
             return True
-        if self.impl != "reference":
-            raise ValueError(f"unknown implementation {self.impl!r}")
         return False
 
     def forward(self, x):
@@ -142,7 +150,9 @@ class FirstPassageAttention(nn.Module):
         self.tau, self.impl, self.block = tau, impl, block
         self.qkv = nn.Linear(d_model, 3 * d_model, bias=False)
         self.out = nn.Linear(d_model, d_model, bias=False)
-        self.field = Field(d_model, n_heads, beta_init, impl=impl)
+        # The layer's impl picks the attention kernels; its Field uses the HIP prologue where that covers
+        # the input (GPU, at most 32 heads) and the PyTorch projection otherwise, as the reference does.
+        self.field = Field(d_model, n_heads, beta_init, impl="reference" if impl == "reference" else None)
 
     def forward(self, x):
         B, T, _ = x.shape

@@ -179,6 +179,9 @@ class FieldHIP(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, weight, bias, n_heads):
         B, T, C = x.shape
+        for name, t in (("weight", weight), ("bias", bias)):
+            if t.device != x.device:
+                raise ValueError(f"Field {name} is on {t.device}, but x is on {x.device}")
         if x.stride(2) != 1:
             x = x.contiguous()
         w = weight.float().contiguous()

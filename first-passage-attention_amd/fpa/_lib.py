@@ -9,6 +9,8 @@ import os
 
 import torch
 
+from ._srchash import source_hash
+
 ABI_VERSION = 3
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libfpa.so")
 
@@ -97,6 +99,11 @@ def lib():
     L.fpa_field_bwd.argtypes = [ctypes.POINTER(FpaFieldBwdArgs), _vp]
     if L.fpa_abi_version() != ABI_VERSION:
         raise RuntimeError(f"libfpa.so ABI {L.fpa_abi_version()} != {ABI_VERSION}: rebuild it")
+    L.fpa_source_hash.restype = ctypes.c_char_p
+    built, here = L.fpa_source_hash().decode(), source_hash()
+    if here is not None and built != here:
+        raise RuntimeError(f"libfpa.so was built from other sources (hash {built}, sources {here}): rebuild it "
+                           "with first-passage-attention_amd/build.py")
     _LIB = L
     return L
 

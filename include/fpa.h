@@ -165,6 +165,11 @@ const char *fpa_last_error(void);
 /* ABI version (bumped whenever the structs above change). */
 int fpa_abi_version(void);
 
+/* Hash of the sources the library was built from (16 hex digits; "unknown" when the build did
+ * not set it).  The Python loader compares it with the sources next to it and refuses a stale
+ * library.  No counterpart in the reference, which compiles its kernels at first call.  */
+const char *fpa_source_hash(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -115,6 +115,86 @@ def fpa_grads(q, k, v, phi, psi, beta, do, tau=1.0, dtype=torch.float64):
     return [o.detach()] + [g.detach() for g in grads]
 
 
+def fpa_grads_chunked(q, k, v, phi, psi, beta, do, tau=1.0, dtype=torch.float64, device=None,
+                      max_elems=1 << 27):
+    """fpa_grads computed over chunks of query rows, for shapes whose (T, T) tensors are too big.
+
+    Same definition (kernel.py:23-64) and the same straight-through autograd formulation: for the
+    query rows t in [t0, t1) of one chunk, keys s < t0 see the ranges (s, t] split at t0,
+
+        min_{s<u<=t} phi_u            = min(SUF_s, PRE_t),   SUF_s = min_{s<u<t0} phi_u,  PRE_t = min_{t0<=u<=t} phi_u
+        log sum_{s<u<=t} e^{-phi_u/tau} = logaddexp(LS_s, LP_t)  (the same split of the log-sum-exp)
+
+    and keys t0 <= s < t1 use the dense formulation restricted to the chunk.  The loss <o, do> is a
+    sum over rows, so each chunk is differentiated on its own and the gradients of k, v, phi, psi
+    and beta accumulate over chunks.  The arithmetic runs in ``dtype`` on ``device`` (default: q's
+    device), so the full-size configurations can be checked in float64 on the GPU; a pass holds at
+    most about ``max_elems`` elements per (t, s) tensor.  Returns CPU tensors like fpa_grads.
+    """
+    dev = torch.device(device) if device is not None else q.device
+    B, H, T, D = q.shape
+    b = beta if torch.is_tensor(beta) else torch.tensor(float(beta))
+    b = b.reshape(-1)
+    if b.numel() == 1:
+        b = b.expand(H)
+    cast = lambda t: t.detach().to(dev, dtype).reshape((B * H,) + tuple(t.shape[2:])).contiguous()  # noqa: E731
+    Q, K, V, PHI, PSI, DO = (cast(t) for t in (q, k, v, phi, psi, do))
+    BETA = b.detach().to(dev, dtype).contiguous()
+    out = [torch.empty_like(Q)] + [torch.zeros_like(x) for x in (Q, K, V, PHI, PSI)]
+    dbeta = torch.zeros(H, dtype=dtype, device=dev)
+    scale = 1.0 / math.sqrt(D)
+    rows = max(1, max_elems // T)                      # (head, query row) pairs per pass
+    G = max(1, min(B * H, rows // min(T, 256)))        # heads per pass (chunks of at least 256 rows)
+    C = max(1, min(T, rows // G))                      # query rows per chunk
+    for h0 in range(0, B * H, G):
+        h1 = min(B * H, h0 + G)
+        heads = torch.arange(h0, h1, device=dev) % H
+        leaves = [x[h0:h1].clone().requires_grad_() for x in (Q, K, V, PHI, PSI)]
+        bet = BETA.clone().requires_grad_()
+        q_, k_, v_, ph, ps = leaves
+        for t0 in range(0, T, C):
+            t1 = min(T, t0 + C)
+            a = -ph[:, :t1] / tau
+            bh = bet[heads].view(-1, 1, 1)
+            # Hard range minimum (no gradient: straight-through, kernel.py:44-54).
+            with torch.no_grad():
+                xin = range_min(ph[:, t0:t1])                                   # (G, C, C), keys in the chunk
+                if t0 > 0:
+                    pre = torch.cummin(ph[:, t0:t1], dim=-1).values             # min over [t0, t]
+                    suf = torch.flip(torch.cummin(torch.flip(ph[:, :t0], [-1]), dim=-1).values, [-1])
+                    suf = torch.cat([suf[:, 1:], torch.full_like(suf[:, :1], math.inf)], dim=-1)  # (s, t0)
+                    xpre = torch.minimum(suf.unsqueeze(-2), pre.unsqueeze(-1))  # (G, C, t0)
+                    hard = torch.cat([xpre, xin], dim=-1)
+                else:
+                    hard = xin
+            # Soft range minimum (carries the gradient), with the reference's finite sentinel.
+            sin = range_softmin(ph[:, t0:t1], tau)
+            if t0 > 0:
+                lp = torch.logcumsumexp(a[:, t0:t1], dim=-1)
+                ls = torch.flip(torch.logcumsumexp(torch.flip(a[:, :t0], [-1]), dim=-1), [-1])
+                ls = torch.cat([ls[:, 1:], torch.full_like(ls[:, :1], -SENTINEL)], dim=-1)
+                spre = -tau * torch.logaddexp(ls.unsqueeze(-2), lp.unsqueeze(-1))
+                soft = torch.cat([spre, sin], dim=-1)
+            else:
+                soft = sin
+            x = hard + (soft - soft.detach()) - ps[:, :t1].unsqueeze(-2)
+            bias = bh * torch.clamp(x, max=0.0)
+            logits = torch.matmul(q_[:, t0:t1], k_[:, :t1].transpose(-1, -2).contiguous()) * scale + bias
+            tt = torch.arange(t0, t1, device=dev).view(-1, 1)
+            ss = torch.arange(0, t1, device=dev).view(1, -1)
+            logits = logits.masked_fill(ss > tt, -math.inf)
+            o_c = torch.matmul(torch.softmax(logits, dim=-1), v_[:, :t1])
+            out[0][h0:h1, t0:t1] = o_c.detach()
+            (o_c * DO[h0:h1, t0:t1]).sum().backward()
+        for i, leaf in enumerate(leaves):
+            out[i + 1][h0:h1] = leaf.grad
+        dbeta += bet.grad
+    shp4, shp3 = (B, H, T, D), (B, H, T)
+    res = [out[0].view(shp4), out[1].view(shp4), out[2].view(shp4), out[3].view(shp4),
+           out[4].view(shp3), out[5].view(shp3), dbeta]
+    return [r.cpu() for r in res]
+
+
 # ----------------------------------------------------------------------------
 # Brute-force restatements used to pin the dense oracle on tiny shapes.
 # ----------------------------------------------------------------------------

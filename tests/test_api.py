@@ -233,3 +233,19 @@ def test_field_workspace_size():
     S = min(64, (B * T + 255) // 256)
     up = lambda n: (n + 63) // 64 * 64
     assert L.fpa_field_workspace_bytes(B, T, C, H) == 4 * (up(B * 3 * H * T + 96) + up(S * 3 * H * (C + 1)))
+
+
+def test_library_is_built_from_these_sources():
+    """libfpa.so carries the hash of the sources it was built from, and it is the hash of the sources
+    in the tree (the loader refuses a stale library)."""
+    from fpa._srchash import source_hash
+    L = _lib.lib()
+    assert L.fpa_source_hash().decode() == source_hash()
+    assert len(source_hash()) == 16
+
+
+def test_field_impl_is_validated():
+    with pytest.raises(ValueError, match="unknown implementation"):
+        fpa.Field(16, 2, impl="cuda")
+    layer = fpa.FirstPassageAttention(64, 2, impl="hip")
+    assert layer.field.impl is None  # the layer's Field picks HIP or PyTorch per input

@@ -313,3 +313,49 @@ def test_graph_replay_matches_eager(fpa):
         assert all(torch.equal(x, y) for x, y in zip(static, eager)), r
         step()  # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_block_is_a_no_op(fpa):
+    """block (the reference's kernel block, test.py:134-147 varies it over 16/32/64) does not change
+    the HIP kernels' results: block = 16, 32, 64 and 128 give bit-identical outputs and gradients."""
+    _say("[parity] block 16/32/64/128 bit-identical, B1 H2 T200 D32 fp16")
+    q, k, v, phi, psi, beta, do = O.make_inputs(1, 2, 200, 32, dtype=torch.float16, seed=81)
+    runs = []
+    for block in (16, 32, 64, 128):
+        a = [t.cuda().clone().requires_grad_() for t in (q, k, v, phi, psi, beta)]
+        o = fpa.first_passage_attention(*a, impl="hip", block=block)
+        runs.append([o.detach()] + list(torch.autograd.grad(o, a, do.cuda())))
+    for other in runs[1:]:
+        assert all(torch.equal(x, y) for x, y in zip(runs[0], other))
+
+
+def test_tensors_on_another_device_are_refused(fpa):
+    """beta (or k, phi, ...) on the CPU with q on the GPU raises ValueError before any launch, as the
+    reference's Triton launch refuses a host tensor."""
+    _say("[api] CPU beta / CPU phi with GPU q")
+    q, k, v, phi, psi, beta, _ = O.make_inputs(1, 2, 64, 32, dtype=torch.float16, seed=82)
+    qd, kd, vd, phid, psid = (t.cuda() for t in (q, k, v, phi, psi))
+    with pytest.raises(ValueError, match="beta is on cpu"):
+        fpa.first_passage_attention(qd, kd, vd, phid, psid, beta, impl="hip")
+    with pytest.raises(ValueError, match="phi is on cpu"):
+        fpa.first_passage_attention(qd, kd, vd, phi, psid, beta.cuda(), impl="hip")
+    with pytest.raises(ValueError, match="k is on cpu"):
+        fpa.first_passage_attention(qd, k, vd, phid, psid, beta.cuda(), impl="hip")
+    torch.cuda.synchronize()
+
+
+def test_layer_with_more_heads_than_the_field_kernels(fpa):
+    """FirstPassageAttention(2048, 64, impl="hip"): 64 heads of D = 32.  The attention runs on the HIP
+    kernels and the Field prologue (HIP kernels up to 32 heads) on PyTorch; output and parameter
+    gradients match the dense layer in fp32."""
+    _say("[layer] 64 heads (d_model 2048, D 32), fp32 hip vs reference")
+    out = []
+    for impl in ("hip", "reference"):
+        torch.manual_seed(0)
+        layer = fpa.FirstPassageAttention(2048, 64, impl=impl).cuda()
+        x = torch.randn(1, 40, 2048, generator=torch.Generator().manual_seed(1)).cuda()
+        y = layer(x)
+        loss = y.float().square().mean()
+        out.append([y.detach().float()] + list(torch.autograd.grad(loss, list(layer.parameters()))))
+    for a, b in zip(*out):
+        assert ((a - b).norm() / b.norm()).item() <= 1e-4

@@ -147,3 +147,23 @@ def test_field_oracle_special_cases():
     p1, s1 = O.field_phi_psi(x1, w1, b1, 1)
     lin = x1[0, 0] @ w1.T + b1
     assert torch.allclose(p1[0, 0, 0], lin[0] + lin[1]) and torch.allclose(s1[0, 0, 0], lin[0] + lin[2])
+
+
+@pytest.mark.parametrize("B,H,T,D,tau,scale,ties,drift,max_elems", [
+    (2, 3, 150, 16, 1.0, 1.0, False, 0.0, 1 << 27),   # one pass: the dense formulation
+    (2, 3, 150, 16, 1.0, 1.0, False, 0.0, 150 * 400),  # two heads per pass
+    (1, 2, 300, 32, 0.7, 3.0, True, 0.0, 300 * 40),   # chunks of 40 rows, ties, tau 0.7
+    (1, 1, 257, 16, 2.0, 40.0, False, 0.0, 257 * 7),  # chunks of 7 rows (ragged), phi scale 40
+    (1, 2, 280, 16, 0.25, 1.0, False, 0.2, 280 * 64),  # steep drift: deep-prefix minima, small tau
+])
+def test_chunked_oracle_is_the_dense_oracle(B, H, T, D, tau, scale, ties, drift, max_elems):
+    """fpa_grads_chunked (query rows in chunks, keys before a chunk through the split range
+    minimum and log-sum-exp) gives the dense oracle's outputs and gradients to 1e-12."""
+    q, k, v, phi, psi, beta, do = O.make_inputs(B, H, T, D, dtype=torch.float32, seed=17, phi_scale=scale,
+                                                ties=ties, drift=drift)
+    ref = O.fpa_grads(q, k, v, phi, psi, beta, do, tau=tau)
+    got = O.fpa_grads_chunked(q, k, v, phi, psi, beta, do, tau=tau, max_elems=max_elems)
+    for name, x, r in zip(("o", "dq", "dk", "dv", "dphi", "dpsi", "dbeta"), got, ref):
+        assert x.shape == r.shape, name
+        assert O.rel_err(x, r) <= 1e-12, (name, O.rel_err(x, r))
+
