@@ -5,6 +5,7 @@
 // kernel.py:390-392, 406-407 and 430-436 so that the caller owns every buffer.
 #include <stdint.h>
 
+#include <mutex>
 #include <string>
 
 #include "fpa.h"
@@ -211,9 +212,13 @@ int fpa_fwd(const FpaFwdArgs *a, void *stream) {
     return FPA_OK;
 }
 
-int fpa_bwd(const FpaBwdArgs *a, void *stream) {
-    g_err.clear();
-    if (a == nullptr) return fail(FPA_ERR_INVALID, "args is NULL");
+}  // extern "C"
+
+namespace {
+
+// The backward of fpa_bwd and fpa_bwd_noalloc: every check but the workspace's, then the launches
+// with their scratch regions carved out of `wsp` (fpa_bwd_workspace_bytes bytes, 256-byte aligned).
+int bwd_impl(const FpaBwdArgs *a, void *wsp, void *stream) {
     int rc = check_common(a->B, a->H, a->T, a->D, a->dtype, a->tau);
     if (rc) return rc;
     if ((rc = check_rows(a->q, a->sq, a->dtype, "q")) || (rc = check_rows(a->k, a->sk, a->dtype, "k")) ||
@@ -224,14 +229,12 @@ int fpa_bwd(const FpaBwdArgs *a, void *stream) {
     if (a->sq[3] != 1 || a->sk[3] != 1 || a->sv[3] != 1 || a->so[3] != 1 || a->sdo[3] != 1 || a->sdq[3] != 1 ||
         a->sdk[3] != 1 || a->sdv[3] != 1)
         return fail(FPA_ERR_INVALID, "the head dimension of every (B, H, T, D) tensor must be contiguous");
-    if (!a->beta || !a->lse || !a->state || !a->dphi || !a->dpsi || !a->dbeta || !a->workspace)
-        return fail(FPA_ERR_INVALID, "beta, lse, state, dphi, dpsi, dbeta and workspace must be non-NULL");
-    if ((reinterpret_cast<uintptr_t>(a->workspace) & 255) != 0)
-        return fail(FPA_ERR_INVALID, "workspace must be 256-byte aligned");
+    if (!a->beta || !a->lse || !a->state || !a->dphi || !a->dpsi || !a->dbeta)
+        return fail(FPA_ERR_INVALID, "beta, lse, state, dphi, dpsi and dbeta must be non-NULL");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int64_t TP = tp_of(a->T);
     const WsLayout wl = ws_layout(a->B, a->H, a->T);
-    float *ws = static_cast<float *>(a->workspace);
+    float *ws = static_cast<float *>(wsp);
     BwdParams p;
     p.q = a->q; p.sq = s3(a->sq);
     p.k = a->k; p.sk = s3(a->sk);
@@ -266,6 +269,69 @@ int fpa_bwd(const FpaBwdArgs *a, void *stream) {
     if ((ph & (FPA_BWD_PHI | FPA_BWD_BETA)) && (e = launch_bwd_combine(p, s)) != hipSuccess)
         return hip_fail(e, "fpa_bwd_combine launch");
     return FPA_OK;
+}
+
+// Scratch of fpa_bwd_noalloc: one array per GPU, placed by the code object's loader (no allocation
+// call), found once per device with hipGetSymbolAddress.  In host code `scratch` names a host-side
+// stand-in, not device memory: only the address in g_scratch_ptr is ever passed on.
+static __device__ __align__(256) char scratch[FPA_NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 256;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[MAX_DEVICES] = {};
+
+// Device address of this GPU's scratch (the current device), or nullptr with the error set.
+void *scratch_of_current_device() {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        hip_fail(e, "fpa_bwd_noalloc: hipGetDevice");
+        return nullptr;
+    }
+    if (dev < 0 || dev >= MAX_DEVICES) {
+        fail(FPA_ERR_UNSUPPORTED, "fpa_bwd_noalloc: device index out of range");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "fpa_bwd_noalloc: hipGetSymbolAddress(scratch)");
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" {
+
+int fpa_bwd(const FpaBwdArgs *a, void *stream) {
+    g_err.clear();
+    if (a == nullptr) return fail(FPA_ERR_INVALID, "args is NULL");
+    if (a->workspace == nullptr) return fail(FPA_ERR_INVALID, "workspace must be non-NULL");
+    if ((reinterpret_cast<uintptr_t>(a->workspace) & 255) != 0)
+        return fail(FPA_ERR_INVALID, "workspace must be 256-byte aligned");
+    return bwd_impl(a, a->workspace, stream);
+}
+
+int fpa_bwd_noalloc(const FpaBwdArgs *a, void *stream) {
+    g_err.clear();
+    if (a == nullptr) return fail(FPA_ERR_INVALID, "args is NULL");
+    int rc = check_common(a->B, a->H, a->T, a->D, a->dtype, a->tau);
+    if (rc) return rc;
+    const int64_t need = ws_layout(a->B, a->H, a->T).total * (int64_t)sizeof(float);
+    if (need > FPA_NOALLOC_SCRATCH_BYTES)
+        return fail(FPA_ERR_UNSUPPORTED, "fpa_bwd_noalloc: this problem needs " + std::to_string(need) +
+                                             " bytes of scratch, more than the " +
+                                             std::to_string((int64_t)FPA_NOALLOC_SCRATCH_BYTES) +
+                                             " it holds; call fpa_bwd with a workspace");
+    void *ws = scratch_of_current_device();
+    if (ws == nullptr) return FPA_ERR_HIP;
+    return bwd_impl(a, ws, stream);
 }
 
 }  // extern "C"

@@ -108,6 +108,11 @@ def run_bwd(args, device):
     _lib.check(_lib.lib().fpa_bwd(args, _lib.stream_of(device)))
 
 
+def run_bwd_noalloc(args, device):
+    """fpa_bwd_noalloc: the backward on the library's static per-GPU scratch (args.workspace unused)."""
+    _lib.check(_lib.lib().fpa_bwd_noalloc(args, _lib.stream_of(device)))
+
+
 class _Saved:
     def __init__(self, o, lse, state):
         self.o, self.lse, self.state = o, lse, state

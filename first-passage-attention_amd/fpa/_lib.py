@@ -18,6 +18,7 @@ FPA_F16, FPA_F32 = 0, 1
 FPA_OK, FPA_ERR_INVALID, FPA_ERR_UNSUPPORTED, FPA_ERR_HIP = 0, 1, 2, 3
 FPA_FWD_STATS, FPA_FWD_MAIN = 1, 2
 FPA_BWD_DELTA, FPA_BWD_KEYS, FPA_BWD_QUERIES, FPA_BWD_PHI, FPA_BWD_BETA = 1, 2, 4, 8, 16
+NOALLOC_SCRATCH_BYTES = 64 << 20  # FPA_NOALLOC_SCRATCH_BYTES of include/fpa.h
 
 _i64 = ctypes.c_int64
 _vp = ctypes.c_void_p
@@ -91,6 +92,8 @@ def lib():
     L.fpa_fwd.argtypes = [ctypes.POINTER(FpaFwdArgs), _vp]
     L.fpa_bwd.restype = ctypes.c_int
     L.fpa_bwd.argtypes = [ctypes.POINTER(FpaBwdArgs), _vp]
+    L.fpa_bwd_noalloc.restype = ctypes.c_int
+    L.fpa_bwd_noalloc.argtypes = [ctypes.POINTER(FpaBwdArgs), _vp]
     L.fpa_field_workspace_bytes.restype = _i64
     L.fpa_field_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64]
     L.fpa_field_fwd.restype = ctypes.c_int
