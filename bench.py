@@ -1,29 +1,29 @@
 #!/usr/bin/env python3
 """Benchmark of First Passage Attention on one MI355X (the BASELINE.json metric).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4]
-    python bench.py --workload lm [--steps K] [--warmup W]     # cfg5 LM training step
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4] [--no-extra] [--no-cpu]
+    python bench.py --workload lm [--steps K] [--warmup W]     # the cfg5 LM training step alone
 
-A step is one forward + backward of ``first_passage_attention(..., impl="hip")`` over
-one batch of synthetic inputs already resident in HBM (BASELINE.json config 2 by
-default: B4 H12 T2048 D64 fp16; q,k,v ~ N(0,1); phi = cumsum N(0,1); psi = phi + N(0,1);
-beta = 1; gradients of o.float().sum() w.r.t. q, k, v, phi, psi, beta).  W untimed
-steps, then K steps timed between two device synchronisations.  Rank 0 prints one
-JSON line.  ``value`` is fwd+bwd TFLOP/s of the algorithmic flops 14*D*P
-(P = B*H*T*(T+1)/2 causal pairs; bias and soft-min work not counted).
+A step is one forward + backward of ``first_passage_attention(..., impl="hip")`` over one batch of
+synthetic inputs already resident in HBM (BASELINE.json config 2 by default: B4 H12 T2048 D64 fp16;
+q,k,v ~ N(0,1); phi = cumsum N(0,1); psi = phi + N(0,1); beta = 1; the gradients of the config's loss
+o.float().sum(), i.e. dO = 1, w.r.t. q, k, v, phi, psi, beta).  W untimed steps, then K steps timed
+between two device synchronisations.  One JSON line.  ``value`` is fwd+bwd TFLOP/s of the algorithmic
+flops 14*D*P (P = B*H*T*(T+1)/2 causal pairs; bias and soft-min work not counted).
+``fwd_bwd_ms_with_clones`` times the reference bench's step (bench.py:46-48 of the reference: fresh
+clones of the six inputs, forward, backward) beside it.
 
-``--workload lm`` times instead one training step (fp16 autocast forward, backward with a
-gradient scaler, AdamW update) of fpa.lm.FPADecoder, a 12-layer d768 H12 pre-norm decoder
-whose attention is the FirstPassageAttention layer on the HIP kernels, over B8 x T2048 random
-tokens (cfg5); ``value`` is tokens per second.
+The default run adds, under ``configs``, the other BASELINE.json workloads: cfg3 and cfg4 (forward and
+forward+backward ms, % of the dtype's MFMA peak) and cfg5 (one training step of fpa.lm.FPADecoder: a
+12-layer d768 H12 pre-norm decoder over B8 x T2048 random tokens, fp16 autocast, gradient scaler,
+AdamW; tokens/s).
 
-Per-kernel times come from HIP events recorded on torch's current stream (the stream
-every kernel is launched on) around C-ABI calls that enqueue one kernel each; the
-dominant kernel's duration gives ``roofline``.  ``roofline.traffic`` is that kernel's HBM
-bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
-(profiles/fpa_<config>_traffic.txt), null when the workload has none.  ``cpu_baseline`` times the float32
-CPU oracle (a port of the reference's dense path) on a bounded sample of heads of
-the same workload.
+Per-kernel times come from HIP events recorded on torch's current stream (the stream every kernel is
+launched on) around C-ABI calls that enqueue one kernel each; the dominant kernel's duration gives
+``roofline``.  ``roofline.traffic`` is that kernel's HBM bytes per launch from the committed rocprofv3
+FETCH_SIZE/WRITE_SIZE summary (profiles/fpa_<config>_traffic.txt), null when there is none.
+``cpu_baseline`` times the float32 CPU oracle (a port of the reference's dense path) on a bounded
+sample of heads of the same workload; ``cpu_baseline_cfg1`` times it on BASELINE.json config 1.
 """
 import argparse
 import json
@@ -42,13 +42,17 @@ METRIC = "FPA fwd & fwd+bwd ms + TFLOP/s (% MFMA peak) at B4 H12 T2048 D64 fp16"
 PEAK_TFLOPS = {"f16": 2516.6, "f32": 157.3}  # MI355X dense MFMA (AMD public figures)
 
 CONFIGS = {
+    "cfg1": dict(B=1, H=2, T=256, D=32, dtype="f32", beta="ones", drift=0.0),
     "cfg2": dict(B=4, H=12, T=2048, D=64, dtype="f16", beta="ones", drift=0.0),
     "cfg3": dict(B=2, H=8, T=4096, D=128, dtype="f32", beta="softplus", drift=0.0),
     "cfg4": dict(B=1, H=12, T=16381, D=64, dtype="f16", beta="ones", drift=0.01),
 }
 
 
-def make_inputs(cfg, seed=0):
+def make_inputs(cfg, seed=0, random_do=False):
+    """(q, k, v, phi, psi, beta, do) of a config, drawn from one CPU generator in the order q, k, v, dO,
+    phi increments, psi noise (then beta for "softplus").  do is the gradient of o.float().sum() (ones)
+    unless random_do."""
     import torch
     dt = torch.float16 if cfg["dtype"] == "f16" else torch.float32
     B, H, T, D = cfg["B"], cfg["H"], cfg["T"], cfg["D"]
@@ -60,6 +64,8 @@ def make_inputs(cfg, seed=0):
         beta = torch.ones(H)
     else:
         beta = torch.nn.functional.softplus(torch.randn(H, generator=g))
+    if not random_do:
+        do = torch.ones_like(do)
     return q, k, v, phi, psi, beta, do
 
 
@@ -79,8 +85,19 @@ def pairs(cfg):
     return cfg["B"] * cfg["H"] * cfg["T"] * (cfg["T"] + 1) // 2
 
 
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(cfg, seconds):
-    """Time the float32 CPU oracle (fwd + bwd of single heads of the workload) for ~`seconds`."""
+    """Time the float32 CPU oracle (fwd + bwd of single heads of the workload) for ~`seconds`, on the
+    host's torch threads (16 on the GPU boxes: OMP_NUM_THREADS)."""
     import torch
     from oracle import fpa_oracle as O
     cores = torch.get_num_threads()
@@ -99,20 +116,42 @@ def cpu_baseline(cfg, seconds):
     t = statistics.median(times)
     flops = 14 * D * T * (T + 1) / 2
     return {"value": flops / t / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
-            "sample": f"{len(times)} x one head (B1 H1 T{T} D{D}) fwd+bwd of the float32 dense oracle, "
-                      f"median {t:.3f} s/head"}
+            "host_cpus": os.cpu_count(), "cpu_model": _cpu_model(),
+            "sample": f"{len(times)} x one head (B1 H1 T{T} D{D}) fwd+bwd of the float32 dense oracle "
+                      f"(dO = 1), median {t:.3f} s/head"}
 
+
+def cpu_baseline_cfg1():
+    """BASELINE.json config 1 (B1 H2 T256 D32 fp32, loss o.sum(), seed 0) forward+backward on the float32
+    CPU oracle: 3 warm-ups, median of 15 (the CPU-baseline plan of BASELINE.md)."""
+    import torch
+    from oracle import fpa_oracle as O
+    q, k, v, phi, psi, beta, do = make_inputs(CONFIGS["cfg1"], seed=0)
+    times = []
+    for i in range(18):
+        t0 = time.perf_counter()
+        O.fpa_grads(q, k, v, phi, psi, beta, do, dtype=torch.float32)
+        if i >= 3:
+            times.append(time.perf_counter() - t0)
+    ms = statistics.median(times) * 1e3
+    return {"ms": round(ms, 3), "cores": torch.get_num_threads(), "host_cpus": os.cpu_count(),
+            "cpu_model": _cpu_model(), "kind": "port",
+            "sample": "B1 H2 T256 D32 fp32 forward+backward of the float32 dense oracle, median of 15"}
+
+
+# The backward kernels of a step: (name, phases bitmask of fpa_bwd, algorithmic flops per causal pair / D).
+# The key side (S, dP, dV, dK: 8 D per pair) and the query side (dQ: 2 D per pair) run as one launch.
+BWD_KERNELS = (("fpa_bwd_prep", 1, 0), ("fpa_bwd_kvq_kernel", 2 | 4, 10), ("fpa_bwd_combine_kernel", 8, 0))
 
 LM = dict(B=8, T=2048, d_model=768, n_heads=12, layers=12, d_mlp=3072, vocab=32000)
 
 
-def run_lm(a):
-    """cfg5: tokens/s of one LM training step (see the module docstring)."""
+def lm_step_ms(steps, warmup):
+    """cfg5: ms per training step of the LM (see the module docstring) and the last loss."""
     import torch
     from fpa.lm import FPADecoder
 
     dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
     torch.manual_seed(0)
     model = FPADecoder(LM["vocab"], LM["d_model"], LM["n_heads"], LM["layers"], LM["d_mlp"], impl="hip").to(dev)
     opt = torch.optim.AdamW(model.parameters(), lr=1e-4)
@@ -129,14 +168,25 @@ def run_lm(a):
         scaler.update()
         return loss
 
-    for _ in range(a.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(a.steps):
+    for _ in range(steps):
         loss = step()
     torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / a.steps
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    loss = loss.item()
+    del model, opt
+    torch.cuda.empty_cache()
+    return ms, loss
+
+
+def run_lm(a):
+    """--workload lm: the cfg5 training step as the bench line."""
+    import torch
+    torch.cuda.set_device(0)
+    ms, loss = lm_step_ms(a.steps, a.warmup)
     ntok = LM["B"] * LM["T"]
     res = {
         "metric": "LM training step tokens/s (cfg5: 12-layer d768 H12 FPA decoder, B8 T2048, fp16 autocast)",
@@ -153,11 +203,50 @@ def run_lm(a):
         "data": "synthetic (uniform random tokens, random-init weights)",
         "config": {"workload": "cfg5: FPADecoder training step (AdamW, grad scaler)", **LM,
                    "parallelism": "single GPU"},
-        "final_loss": round(loss.item(), 4),
+        "final_loss": round(loss, 4),
         "roofline": None,
         "cpu_baseline": None,
     }
     print(json.dumps(res), flush=True)
+
+
+def time_steps(fn, steps, warmup):
+    """ms per call of fn over `steps` back-to-back calls between two device synchronisations."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def time_config(cfg, steps, warmup):
+    """Forward and forward+backward ms of one config (inputs resident, leaves kept across steps)."""
+    import torch
+    import fpa
+    dev = torch.device("cuda:0")
+    q, k, v, phi, psi, beta, do = (t.to(dev) for t in make_inputs(cfg))
+    leaves = [t.clone().requires_grad_() for t in (q, k, v, phi, psi, beta)]
+
+    def step():
+        o = fpa.first_passage_attention(*leaves, impl="hip")
+        torch.autograd.grad(o, leaves, do)
+
+    def fwd():
+        with torch.no_grad():
+            fpa.first_passage_attention(q, k, v, phi, psi, beta, impl="hip")
+
+    fb = time_steps(step, steps, warmup)
+    f = time_steps(fwd, steps, warmup)
+    P, D = pairs(cfg), cfg["D"]
+    peak = PEAK_TFLOPS[cfg["dtype"]]
+    return {"workload": f"B{cfg['B']} H{cfg['H']} T{cfg['T']} D{D} {cfg['dtype']}",
+            "fwd_ms": round(f, 4), "fwd_bwd_ms": round(fb, 4),
+            "fwd_pct_peak": round(100 * 4 * D * P / (f * 1e-3) / 1e12 / peak, 2),
+            "fwd_bwd_pct_peak": round(100 * 14 * D * P / (fb * 1e-3) / 1e12 / peak, 2)}
 
 
 def main():
@@ -165,12 +254,13 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="cfg2", choices=[c for c in sorted(CONFIGS) if c != "cfg1"])
     ap.add_argument("--workload", default="fpa", choices=("fpa", "lm"),
                     help="fpa: the attention forward+backward of --config; lm: the cfg5 LM training step")
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline legs")
+    ap.add_argument("--no-extra", action="store_true", help="skip the other configs (cfg3, cfg4, cfg5)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="first run one device-to-device copy of this many MiB (a known-size kernel that "
                          "calibrates the FETCH_SIZE / WRITE_SIZE counters of a profiling run)")
@@ -199,20 +289,19 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     q, k, v, phi, psi, beta, do = (t.to(dev) for t in make_inputs(cfg))
-    leaves = [t.clone().requires_grad_() for t in (q, k, v, phi, psi, beta)]
+    inputs = (q, k, v, phi, psi, beta)
+    leaves = [t.clone().requires_grad_() for t in inputs]
 
     def step():
         o = fpa.first_passage_attention(*leaves, impl="hip")
         torch.autograd.grad(o, leaves, do)
 
-    for _ in range(a.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(a.steps):
-        step()
-    torch.cuda.synchronize()
-    fwd_bwd_ms = (time.perf_counter() - t0) * 1e3 / a.steps
+    def step_with_clones():  # the reference bench's step (its bench.py:46-48)
+        x = [t.clone().requires_grad_() for t in inputs]
+        fpa.first_passage_attention(*x, impl="hip").backward(do)
+
+    fwd_bwd_ms = time_steps(step, a.steps, a.warmup)
+    clones_ms = time_steps(step_with_clones, a.steps, a.warmup)
 
     # The same step captured once in a HIP graph and replayed: the kernels without the host's
     # launch gaps (reported beside the eager step, which stays the bench value).
@@ -225,25 +314,14 @@ def main():
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         step()
-    for _ in range(a.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(a.steps):
-        graph.replay()
-    torch.cuda.synchronize()
-    graph_ms = (time.perf_counter() - t0) * 1e3 / a.steps
+    graph_ms = time_steps(graph.replay, a.steps, a.warmup)
     del graph
 
-    with torch.no_grad():
-        for _ in range(a.warmup):
-            fpa.first_passage_attention(q, k, v, phi, psi, beta, impl="hip")
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(a.steps):
-            fpa.first_passage_attention(q, k, v, phi, psi, beta, impl="hip")
-        torch.cuda.synchronize()
-        fwd_ms = (time.perf_counter() - t0) * 1e3 / a.steps
+    def fwd():
+        with torch.no_grad():
+            fpa.first_passage_attention(*inputs, impl="hip")
+
+    fwd_ms = time_steps(fwd, a.steps, a.warmup)
 
     # Per-kernel durations: one C-ABI call per kernel (phases), HIP events on the launch stream.
     qr, kr, vr = _hip.rows(q), _hip.rows(k), _hip.rows(v)
@@ -270,18 +348,13 @@ def main():
 
     P = pairs(cfg)
     D = cfg["D"]
-    # The kernels of a step, with their algorithmic flops.  The backward's key side (S, dP, dV, dK:
-    # 8*D per pair) and query side (dQ: 2*D per pair; it recomputes S and dP) run as one launch.
+    # The kernels of a step, with their algorithmic flops.
     kernels = {
         "fpa_stats": (time_call(fa, _hip.run_fwd, _lib.FPA_FWD_STATS), 0),
         "fpa_fwd_kernel": (time_call(fa, _hip.run_fwd, _lib.FPA_FWD_MAIN), 4 * D * P),
-        "fpa_bwd_prep": (time_call(ba, _hip.run_bwd, _lib.FPA_BWD_DELTA), 0),
-        "fpa_bwd_kvq_kernel": (time_call(ba, _hip.run_bwd, _lib.FPA_BWD_KEYS | _lib.FPA_BWD_QUERIES), 10 * D * P),
-        "fpa_bwd_combine_kernel": (time_call(ba, _hip.run_bwd, _lib.FPA_BWD_PHI), 0),
     }
-    # Each side launched alone (not part of the step): for comparison with the fused launch.
-    alone = {"fpa_bwd_kv_kernel": time_call(ba, _hip.run_bwd, _lib.FPA_BWD_KEYS),
-             "fpa_bwd_q_kernel": time_call(ba, _hip.run_bwd, _lib.FPA_BWD_QUERIES)}
+    for name, phases, flops in BWD_KERNELS:
+        kernels[name] = (time_call(ba, _hip.run_bwd, phases), flops * D * P)
     dom = max(kernels, key=lambda n: kernels[n][0])
     dom_ms, dom_flops = kernels[dom]
     peak = PEAK_TFLOPS[cfg["dtype"]]
@@ -290,10 +363,25 @@ def main():
     fwd_flops, fb_flops = 4 * D * P, 14 * D * P
     fb_tflops = fb_flops / (fwd_bwd_ms * 1e-3) / 1e12
     fwd_tflops = fwd_flops / (fwd_ms * 1e-3) / 1e12
+    del fb, gb, fa, ba, leaves, q, k, v, phi, psi, beta, do, inputs
+    torch.cuda.empty_cache()
 
-    cpu = None
+    extra = {}
+    if not a.no_extra:
+        for name in ("cfg3", "cfg4"):
+            if name != a.config:
+                extra[name] = time_config(CONFIGS[name], 10, 3)
+                torch.cuda.empty_cache()
+        lm_ms, lm_loss = lm_step_ms(5, 2)
+        extra["cfg5"] = {"workload": "FPADecoder training step: 12 layers d768 H12, B8 T2048, fp16 autocast, AdamW",
+                         "ms_per_step": round(lm_ms, 3),
+                         "tokens_per_s": round(LM["B"] * LM["T"] / (lm_ms * 1e-3), 1),
+                         "loss": round(lm_loss, 4)}
+
+    cpu = cpu1 = None
     if not a.no_cpu:
         cpu = cpu_baseline(cfg, a.cpu_seconds)
+        cpu1 = cpu_baseline_cfg1()
 
     res = {
         "metric": METRIC,
@@ -309,20 +397,24 @@ def main():
         "dtype": cfg["dtype"],
         "data": "synthetic",
         "config": {"workload": f"{a.config}: FPA forward+backward B{cfg['B']} H{cfg['H']} T{cfg['T']} "
-                               f"D{cfg['D']} {cfg['dtype']}",
+                               f"D{cfg['D']} {cfg['dtype']}, dO = 1 (loss o.float().sum())",
                    "B": cfg["B"], "H": cfg["H"], "T": cfg["T"], "D": D, "parallelism": "single GPU"},
         "fwd_ms": round(fwd_ms, 4),
         "fwd_bwd_ms": round(fwd_bwd_ms, 4),
+        "fwd_bwd_ms_with_clones": round(clones_ms, 4),
         "fwd_bwd_graph_ms": round(graph_ms, 4),
         "fwd_tflops": round(fwd_tflops, 3),
         "fwd_pct_peak": round(100 * fwd_tflops / peak, 2),
         "fwd_bwd_pct_peak": round(100 * fb_tflops / peak, 2),
         "kernel_ms": {n: round(t, 4) for n, (t, _) in kernels.items()},
-        "kernel_ms_alone": {n: round(t, 4) for n, t in alone.items()},
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 3), "peak": peak,
                      "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
-                     "traffic": measured_traffic(a.config, dom)},
+                     "traffic": measured_traffic(a.config, dom),
+                     "note": "priced against the dense MFMA peak of the dtype; the kernel's own limiter "
+                             "(VALU issue or MFMA) is in profiles/fpa_<config>_counters.md"},
+        "configs": extra,
         "cpu_baseline": cpu,
+        "cpu_baseline_cfg1": cpu1,
     }
     print(json.dumps(res), flush=True)
 
