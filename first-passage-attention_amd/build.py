@@ -51,7 +51,8 @@ def _srchash():
 
 def _compile(src, defs=()):
     obj = os.path.join(BUILD, os.path.basename(src).replace(".hip", ".o"))
-    cmd = [hipcc()] + COMMON + list(defs) + PER_FILE.get(os.path.basename(src), []) + ["-c", src, "-o", obj]
+    extra = os.environ.get("FPA_HIPCC_FLAGS", "").split()  # tuning experiments: extra -D / -mllvm flags
+    cmd = [hipcc()] + COMMON + list(defs) + PER_FILE.get(os.path.basename(src), []) + extra + ["-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stdout}\n{r.stderr}")
