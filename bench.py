@@ -140,9 +140,9 @@ def cpu_baseline_cfg1():
 
 
 # The backward kernels of a step: (name, phases bitmask of fpa_bwd, algorithmic flops per causal pair / D).
-# The single-pass kernel computes S, dP, dV, dK and the partial dQ (10 D per pair); the combine kernel adds
-# the dQ partials and computes dphi and dbeta.
-BWD_KERNELS = (("fpa_bwd_prep", 1, 0), ("fpa_bwd_main_kernel", 2 | 4, 10), ("fpa_bwd_combine_kernel", 8, 0))
+# The key side (S, dP, dV, dK: 8 D per pair) and the query side (dQ: 2 D per pair; it recomputes S and
+# dP) run as one launch.
+BWD_KERNELS = (("fpa_bwd_prep", 1, 0), ("fpa_bwd_kvq_kernel", 2 | 4, 10), ("fpa_bwd_combine_kernel", 8, 0))
 
 LM = dict(B=8, T=2048, d_model=768, n_heads=12, layers=12, d_mlp=3072, vocab=32000)
 

@@ -27,23 +27,19 @@ int64_t tp_of(int64_t T) { return ((T + G - 1) / G) * G; }
 int64_t align64(int64_t n) { return (n + 63) / 64 * 64; }  // floats -> 256-byte multiple
 
 struct WsLayout {
-    int64_t qinfo, wsum, rsum, gd, tbuf, dbp, dqp, rp, total;  // float offsets
-    int nkt;  // key tiles of the single-pass backward (0: the two-sided kernels run)
+    int64_t qinfo, wsum, rsum, gd, tbuf, dbp, total;  // float offsets
 };
 
-WsLayout ws_layout(int64_t B, int64_t H, int64_t T, int64_t D, int32_t dtype) {
+WsLayout ws_layout(int64_t B, int64_t H, int64_t T) {
     const int64_t BH = B * H, TP = tp_of(T), NB = TP / G, NK32 = (T + 31) / 32;
     WsLayout w;
-    w.nkt = main_bwd_covers(dtype, (int)D) ? (int)((T + MAIN_BK - 1) / MAIN_BK) : 0;
     int64_t off = 0;
     w.qinfo = off; off += align64((int64_t)QI_PLANES * BH * TP);
     w.wsum = off;  off += align64(BH * TP);
-    w.rsum = off;  off += align64(w.nkt ? 0 : BH * TP);
+    w.rsum = off;  off += align64(BH * TP);
     w.gd = off;    off += align64(BH * NB * G * G);
     w.tbuf = off;  off += align64(BH * NB * NB * 2);
     w.dbp = off;   off += align64(BH * NK32);
-    w.dqp = off;   off += align64(w.nkt ? BH * dqp_per_head((int)NB, w.nkt, MAIN_BK / G) * G * D : 0);
-    w.rp = off;    off += align64(BH * w.nkt * TP);
     w.total = off;
     return w;
 }
@@ -131,7 +127,9 @@ int64_t fpa_state_floats(int64_t B, int64_t H, int64_t T) {
 int64_t fpa_lse_floats(int64_t B, int64_t H, int64_t T) { return B * H * tp_of(T); }
 
 int64_t fpa_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D, int32_t dtype) {
-    return ws_layout(B, H, T, D, dtype).total * (int64_t)sizeof(float);
+    (void)D;
+    (void)dtype;
+    return ws_layout(B, H, T).total * (int64_t)sizeof(float);
 }
 
 int64_t fpa_field_workspace_bytes(int64_t B, int64_t T, int64_t C, int64_t H) {
@@ -235,7 +233,7 @@ int bwd_impl(const FpaBwdArgs *a, void *wsp, void *stream) {
         return fail(FPA_ERR_INVALID, "beta, lse, state, dphi, dpsi and dbeta must be non-NULL");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int64_t TP = tp_of(a->T);
-    const WsLayout wl = ws_layout(a->B, a->H, a->T, a->D, a->dtype);
+    const WsLayout wl = ws_layout(a->B, a->H, a->T);
     float *ws = static_cast<float *>(wsp);
     BwdParams p;
     p.q = a->q; p.sq = s3(a->sq);
@@ -251,7 +249,6 @@ int bwd_impl(const FpaBwdArgs *a, void *wsp, void *stream) {
     p.qinfo = ws + wl.qinfo;
     p.wsum = ws + wl.wsum; p.rsum = ws + wl.rsum;
     p.gd = ws + wl.gd; p.tbuf = ws + wl.tbuf; p.dbp = ws + wl.dbp;
-    p.dqp = ws + wl.dqp; p.rp = ws + wl.rp; p.nkt = wl.nkt; p.D = (int)a->D;
     p.B = (int)a->B; p.H = (int)a->H; p.T = (int)a->T; p.TP = (int)TP; p.NB = (int)(TP / G);
     p.BH = (int)(a->B * a->H); p.NK32 = (int)((a->T + 31) / 32);
     p.sc2 = LOG2E / sqrtf((float)a->D);
@@ -261,10 +258,7 @@ int bwd_impl(const FpaBwdArgs *a, void *wsp, void *stream) {
     hipError_t e;
     if ((ph & FPA_BWD_DELTA) && (e = launch_bwd_prep(p, a->dtype, (int)a->D, s)) != hipSuccess)
         return hip_fail(e, "fpa_bwd_prep launch");
-    if (p.nkt > 0) {  // one pass over the pairs: both sides in one kernel
-        if ((ph & (FPA_BWD_KEYS | FPA_BWD_QUERIES)) && (e = launch_bwd_main(p, a->dtype, (int)a->D, s)) != hipSuccess)
-            return hip_fail(e, "fpa_bwd_main launch");
-    } else if ((ph & FPA_BWD_KEYS) && (ph & FPA_BWD_QUERIES)) {
+    if ((ph & FPA_BWD_KEYS) && (ph & FPA_BWD_QUERIES)) {
         if ((e = launch_bwd_kvq(p, a->dtype, (int)a->D, s)) != hipSuccess) return hip_fail(e, "fpa_bwd_kvq launch");
     } else {
         if ((ph & FPA_BWD_KEYS) && (e = launch_bwd_kv(p, a->dtype, (int)a->D, s)) != hipSuccess)
@@ -272,7 +266,7 @@ int bwd_impl(const FpaBwdArgs *a, void *wsp, void *stream) {
         if ((ph & FPA_BWD_QUERIES) && (e = launch_bwd_q(p, a->dtype, (int)a->D, s)) != hipSuccess)
             return hip_fail(e, "fpa_bwd_q launch");
     }
-    if ((ph & (FPA_BWD_PHI | FPA_BWD_BETA)) && (e = launch_bwd_combine(p, a->dtype, s)) != hipSuccess)
+    if ((ph & (FPA_BWD_PHI | FPA_BWD_BETA)) && (e = launch_bwd_combine(p, s)) != hipSuccess)
         return hip_fail(e, "fpa_bwd_combine launch");
     return FPA_OK;
 }
@@ -329,7 +323,7 @@ int fpa_bwd_noalloc(const FpaBwdArgs *a, void *stream) {
     if (a == nullptr) return fail(FPA_ERR_INVALID, "args is NULL");
     int rc = check_common(a->B, a->H, a->T, a->D, a->dtype, a->tau);
     if (rc) return rc;
-    const int64_t need = ws_layout(a->B, a->H, a->T, a->D, a->dtype).total * (int64_t)sizeof(float);
+    const int64_t need = ws_layout(a->B, a->H, a->T).total * (int64_t)sizeof(float);
     if (need > FPA_NOALLOC_SCRATCH_BYTES)
         return fail(FPA_ERR_UNSUPPORTED, "fpa_bwd_noalloc: this problem needs " + std::to_string(need) +
                                              " bytes of scratch, more than the " +

@@ -82,35 +82,7 @@ __device__ __forceinline__ float block_sum_256(float x, float *red, int w, int l
     return r;
 }
 
-// dq of block U from the partial dQ of the single-pass backward: the key tiles' partials added in
-// ascending tile order, scaled by 1 / sqrt(D), written in q's dtype through dq's strides.
-template <typename T>
-__device__ __forceinline__ void reduce_dq(const BwdParams &p, int U, int bh, int tid) {
-    constexpr int BPT = MAIN_BK / G;
-    const int b = bh / p.H, h = bh % p.H;
-    const int ktmax = min(p.nkt - 1, U / BPT);
-    const int64_t per_head = dqp_per_head(p.NB, p.nkt, BPT);
-    const int D = p.D, n4 = G * D / 4;
-    T *dqb = static_cast<T *>(p.dq) + b * p.sdq.b + h * p.sdq.h;
-    for (int i = tid; i < n4; i += NTHREADS) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (int kt = 0; kt <= ktmax; ++kt)
-            acc += reinterpret_cast<const f32x4 *>(p.dqp + dqp_block(bh, kt, U, p.NB, BPT, per_head) * (G * D))[i];
-        const int row = 4 * i / D, col = 4 * i % D, t = U * G + row;
-        if (t < p.T) {
-            T *dst = dqb + (int64_t)t * p.sdq.t + col;
-            if constexpr (sizeof(T) == 2) {
-                *reinterpret_cast<h4 *>(dst) = h4{(f16)(acc[0] * p.smscale), (f16)(acc[1] * p.smscale),
-                                                  (f16)(acc[2] * p.smscale), (f16)(acc[3] * p.smscale)};
-            } else {
-                *reinterpret_cast<f32x4 *>(dst) = acc * p.smscale;
-            }
-        }
-    }
-}
-
 // Dynamic LDS: sBM, scanA, scanB, NB floats each.
-template <typename T>
 __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) {
     extern __shared__ float dyn[];
     __shared__ float sA[G], sC[G], sc[G], sW[G], sR[G];
@@ -159,14 +131,7 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
         sC[tid] = (suf < pinf()) ? -suf * il2 : ninf();
         sc[tid] = (pre < pinf()) ? -pre * il2 : ninf();
         sW[tid] = p.wsum[r];
-        if (p.nkt > 0) {  // the key tiles' soft-min row sums, in ascending tile order
-            const int ktmax = min(p.nkt - 1, U / (MAIN_BK / G));
-            float rr = 0.f;
-            for (int kt = 0; kt <= ktmax; ++kt) rr += p.rp[((int64_t)bh * p.nkt + kt) * p.TP + sb + tid];
-            sR[tid] = rr;
-        } else {
-            sR[tid] = p.rsum[r];
-        }
+        sR[tid] = p.rsum[r];
     }
     for (int i = tid; i < NB; i += NTHREADS) sBM[i] = -p.state[L.bplane(BP_MIN) + brow + i] * il2;
     __syncthreads();
@@ -354,15 +319,11 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
             p.dphi[(int64_t)bh * p.T + sb + u] = p.beta[h] * tot;
         }
     }
-    if (p.nkt > 0) reduce_dq<T>(p, U, bh, tid);
 }
 
-hipError_t launch_bwd_combine(const BwdParams &p, int dtype, hipStream_t s) {
+hipError_t launch_bwd_combine(const BwdParams &p, hipStream_t s) {
     const size_t dyn = 3 * (size_t)p.NB * sizeof(float);
-    if (dtype == 0)
-        hipLaunchKernelGGL(fpa_bwd_combine_kernel<f16>, dim3(p.NB, p.BH), dim3(NTHREADS), dyn, s, p);
-    else
-        hipLaunchKernelGGL(fpa_bwd_combine_kernel<float>, dim3(p.NB, p.BH), dim3(NTHREADS), dyn, s, p);
+    hipLaunchKernelGGL(fpa_bwd_combine_kernel, dim3(p.NB, p.BH), dim3(NTHREADS), dyn, s, p);
     return hipGetLastError();
 }
 

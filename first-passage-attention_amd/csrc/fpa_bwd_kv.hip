@@ -44,8 +44,6 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_prep_kernel(BwdParams p) {
         p.qinfo[qi_at(bh, p.NB, row, QI_DL)] = ok ? -acc : 0.f;
         p.qinfo[qi_at(bh, p.NB, row, QI_PRE)] = ok ? p.state[L.at(PL_PRE, bh, row)] : pinf();
         p.qinfo[qi_at(bh, p.NB, row, QI_ZQ)] = (FPA_KV_PROD && spread <= PROD_SPREAD) ? fexp2(prl) : prl;
-        p.qinfo[qi_at(bh, p.NB, row, QI_PREL)] = ok ? p.state[L.at(PL_PREL, bh, row)] : 0.f;
-        p.qinfo[qi_at(bh, p.NB, row, QI_CT)] = ok ? -p.state[L.at(PL_PRE, bh, row)] * p.il2 : 0.f;
         // The block's BMIN and BLSE for the key side's loop (plane 7, positions 0 and 1).
         if (row % G < 2) p.qinfo[qi_at(bh, p.NB, row, QI_BST)] = (row % G == 0) ? p.state[L.bplane(BP_MIN) + (int64_t)bh * p.NB + row / G] : blse;
     }

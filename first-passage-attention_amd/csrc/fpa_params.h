@@ -54,12 +54,6 @@ struct BwdParams {
     float *gd;     // BH * NB * G * G   gated dS of in-block pairs, [s][t]
     float *tbuf;   // BH * NB * NB * 2  middle-block sums (two 32-key halves)
     float *dbp;    // BH * NK32         dbeta partials, one per 32-key group
-    // single-pass backward (fp16, D <= 64): per key tile of 256 keys, the partial dQ of each query
-    // block it covers (64 x D floats, dqp_block()) and its soft-min row sums R (TP floats)
-    float *dqp;
-    float *rp;
-    int nkt;       // key tiles of the single-pass backward; 0 when the two-sided kernels run
-    int D;
     int B, H, T, TP, NB, BH, NK32;
     float sc2;     // log2(e) / sqrt(D)
     float smscale; // 1 / sqrt(D)
@@ -82,10 +76,8 @@ struct FieldParams {
 
 // BwdParams::qinfo holds, per 64-query block of a head, QI_PLANES planes of 64 floats
 // ([bh][block][plane][64]), so the key side stages a block's first four planes with one 1 KB load.
-// QI_BST holds the block's BMIN and BLSE at positions 0 and 1.  QI_PREL is PREL_t and QI_CT is
-// c_t = -PRE_t log2(e) / tau (both 0 past T, so the exact soft-min terms of those rows stay finite);
-// plane 7 is unused.
-enum { QI_LQ = 0, QI_DL = 1, QI_PRE = 2, QI_ZQ = 3, QI_BST = 4, QI_PREL = 5, QI_CT = 6, QI_PLANES = 8 };
+// QI_BST holds the block's BMIN and BLSE at positions 0 and 1; planes 5-7 are unused.
+enum { QI_LQ = 0, QI_DL = 1, QI_PRE = 2, QI_ZQ = 3, QI_BST = 4, QI_PLANES = 8 };
 __host__ __device__ inline int64_t qi_at(int64_t bh, int NB, int row, int plane) {
     return ((bh * NB + row / 64) * QI_PLANES + plane) * 64 + row % 64;
 }
@@ -97,29 +89,7 @@ hipError_t launch_bwd_prep(const BwdParams &p, int dtype, int D, hipStream_t s);
 hipError_t launch_bwd_kv(const BwdParams &p, int dtype, int D, hipStream_t s);
 hipError_t launch_bwd_q(const BwdParams &p, int dtype, int D, hipStream_t s);
 hipError_t launch_bwd_kvq(const BwdParams &p, int dtype, int D, hipStream_t s);  // both sides, one launch
-hipError_t launch_bwd_main(const BwdParams &p, int dtype, int D, hipStream_t s);  // single pass (fp16, D <= 64)
-hipError_t launch_bwd_combine(const BwdParams &p, int dtype, hipStream_t s);
-
-// Offset (in blocks of 64 x D floats) of the partial dQ of key tile kt for query block ib of head
-// bh: the tiles of a head are stored one after the other, tile kt holding blocks kt * BPT .. NB - 1.
-__host__ __device__ inline int64_t dqp_block(int64_t bh, int kt, int ib, int NB, int BPT, int64_t per_head) {
-    const int64_t base = (int64_t)kt * NB - (int64_t)BPT * kt * (kt - 1) / 2;
-    return bh * per_head + base + (ib - kt * BPT);
-}
-// Blocks of partial dQ per head.
-__host__ __device__ inline int64_t dqp_per_head(int NB, int NKT, int BPT) {
-    return (int64_t)NKT * NB - (int64_t)BPT * NKT * (NKT - 1) / 2;
-}
-
-// Whether the single-pass backward covers (dtype, D); the two-sided kernels run otherwise.
-#ifndef FPA_MAIN_BWD
-#define FPA_MAIN_BWD 1
-#endif
-inline bool main_bwd_covers(int dtype, int D) { return FPA_MAIN_BWD && dtype == 0 && (D == 16 || D == 32 || D == 64); }
-#ifndef FPA_MAIN_BK
-#define FPA_MAIN_BK 256
-#endif
-constexpr int MAIN_BK = FPA_MAIN_BK;  // keys per workgroup of the single-pass backward (32 per wave)
+hipError_t launch_bwd_combine(const BwdParams &p, hipStream_t s);
 hipError_t launch_field_fwd(const FieldParams &p, int dtype, hipStream_t s);
 hipError_t launch_field_bwd(const FieldParams &p, int dtype, hipStream_t s);
 

@@ -18,7 +18,7 @@ FPA_F16, FPA_F32 = 0, 1
 FPA_OK, FPA_ERR_INVALID, FPA_ERR_UNSUPPORTED, FPA_ERR_HIP = 0, 1, 2, 3
 FPA_FWD_STATS, FPA_FWD_MAIN = 1, 2
 FPA_BWD_DELTA, FPA_BWD_KEYS, FPA_BWD_QUERIES, FPA_BWD_PHI, FPA_BWD_BETA = 1, 2, 4, 8, 16
-NOALLOC_SCRATCH_BYTES = 256 << 20  # FPA_NOALLOC_SCRATCH_BYTES of include/fpa.h
+NOALLOC_SCRATCH_BYTES = 64 << 20  # FPA_NOALLOC_SCRATCH_BYTES of include/fpa.h
 
 _i64 = ctypes.c_int64
 _vp = ctypes.c_void_p

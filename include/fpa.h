@@ -166,7 +166,7 @@ int fpa_bwd(const FpaBwdArgs *args, void *stream);
  * ends.  Problems whose fpa_bwd_workspace_bytes exceed it return FPA_ERR_UNSUPPORTED before any
  * launch.  Calls that overlap on one GPU (two streams, two threads) share that array and race:
  * serialise them.  Allocates nothing (no hipMalloc or allocating library routine).            */
-#define FPA_NOALLOC_SCRATCH_BYTES (256ll << 20)
+#define FPA_NOALLOC_SCRATCH_BYTES (64ll << 20)
 int fpa_bwd_noalloc(const FpaBwdArgs *args, void *stream);
 
 /* Message of the last failed call on this host thread ("" if none). */
