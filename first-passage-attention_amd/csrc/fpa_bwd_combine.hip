@@ -91,7 +91,7 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
     __shared__ float sF[G], sH[G];           // single-reference key-block and query-block terms
     __shared__ float red[4];
 
-    const int U = group_x(), bh = group_y(), b = bh / p.H, h = bh % p.H;
+    const int U = group_x(), bh = group_bh(p.H), b = bh / p.H, h = bh % p.H;
     const int tid = thread_x(), lane = tid % 64;
     const int w = __builtin_amdgcn_readfirstlane(tid / 64);
     const int sb = U * G, last = min(G - 1, p.T - 1 - sb);
@@ -323,7 +323,13 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
 
 hipError_t launch_bwd_combine(const BwdParams &p, hipStream_t s) {
     const size_t dyn = 3 * (size_t)p.NB * sizeof(float);
-    hipLaunchKernelGGL(fpa_bwd_combine_kernel, dim3(p.NB, p.BH), dim3(NTHREADS), dyn, s, p);
+    if (dyn > 48 * 1024) {  // above the default dynamic LDS allowance: raise it once per process
+        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&fpa_bwd_combine_kernel),
+                                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                           3 * MAX_NB * (int)sizeof(float));
+        if (attr != hipSuccess) return attr;
+    }
+    hipLaunchKernelGGL(fpa_bwd_combine_kernel, head_grid(p.NB, p.H, p.BH), dim3(NTHREADS), dyn, s, p);
     return hipGetLastError();
 }
 

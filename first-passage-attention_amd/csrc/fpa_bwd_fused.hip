@@ -44,7 +44,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WP
 fpa_bwd_kvq_kernel(BwdParams p, BwdOrder ord) {
     __shared__ BwdShared<T, D, NW> sm;
     int slot, bh;
-    xcd_work_item(slot, bh, p.BH, 2 * ((p.T + 32 * NW - 1) / (32 * NW)));
+    xcd_work_item(slot, bh, p.BH, p.H, 2 * ((p.T + 32 * NW - 1) / (32 * NW)));
     const int e = __builtin_amdgcn_readfirstlane((int)ord.e[slot]);
     if (e & 0x8000)
         bwd_q_tile<T, D, NW>(p, sm.q, e & 0x7fff, bh);
@@ -56,24 +56,30 @@ template <typename T, int D>
 static hipError_t launch_kvq_t(const BwdParams &p, hipStream_t s) {
     constexpr int NW = FPA_NW, BT = 32 * NW, WPE = kv_wpe<T, D>();
     const int nt = (p.T + BT - 1) / BT;  // key tiles; as many query tiles
-    if (WPE != q_wpe<T, D>() || 2 * nt > FUSED_MAX) {  // no common launch shape: two launches
+    auto two_launches = [&]() {
         hipError_t e = launch_bwd_kv(p, sizeof(T) == 2 ? 0 : 1, D, s);
         return e != hipSuccess ? e : launch_bwd_q(p, sizeof(T) == 2 ? 0 : 1, D, s);
+    };
+    if constexpr (WPE != q_wpe<T, D>() || kv_parts<T, D>() > 1) {  // no common launch shape
+        return two_launches();
+    } else {
+        if (2 * nt > FUSED_MAX) return two_launches();
+        // Block iterations of key tile kt (query blocks from its diagonal block to the end) and of
+        // query tile qt (key blocks from its diagonal block down to 0), weighted by their cost.
+        auto c_kv = [&](int kt) { return FPA_FUSE_WKV * (p.NB - kt * BT / G); };
+        auto c_q = [&](int qt) { return FPA_FUSE_WQ * (std::min(p.NB - 1, (qt * BT + BT - 1) / G) + 1); };
+        BwdOrder ord;
+        int n = 0;
+        for (int kt = 0, qt = nt - 1; kt < nt || qt >= 0;) {  // merge, costliest first
+            if (qt < 0 || (kt < nt && c_kv(kt) >= c_q(qt)))
+                ord.e[n++] = (uint16_t)kt++;
+            else
+                ord.e[n++] = (uint16_t)(0x8000 | qt--);
+        }
+        hipLaunchKernelGGL((fpa_bwd_kvq_kernel<T, D, WPE, NW>), head_grid(2 * nt, p.H, p.BH), dim3(64 * NW), 0, s, p,
+                           ord);
+        return hipGetLastError();
     }
-    // Block iterations of key tile kt (query blocks from its diagonal block to the end) and of
-    // query tile qt (key blocks from its diagonal block down to 0), weighted by their cost.
-    auto c_kv = [&](int kt) { return FPA_FUSE_WKV * (p.NB - kt * BT / G); };
-    auto c_q = [&](int qt) { return FPA_FUSE_WQ * (std::min(p.NB - 1, (qt * BT + BT - 1) / G) + 1); };
-    BwdOrder ord;
-    int n = 0;
-    for (int kt = 0, qt = nt - 1; kt < nt || qt >= 0;) {  // merge, costliest first
-        if (qt < 0 || (kt < nt && c_kv(kt) >= c_q(qt)))
-            ord.e[n++] = (uint16_t)kt++;
-        else
-            ord.e[n++] = (uint16_t)(0x8000 | qt--);
-    }
-    hipLaunchKernelGGL((fpa_bwd_kvq_kernel<T, D, WPE, NW>), dim3(2 * nt, p.BH), dim3(64 * NW), 0, s, p, ord);
-    return hipGetLastError();
 }
 
 hipError_t launch_bwd_kvq(const BwdParams &p, int dtype, int D, hipStream_t s) {
@@ -83,6 +89,7 @@ hipError_t launch_bwd_kvq(const BwdParams &p, int dtype, int D, hipStream_t s) {
             case 32: return launch_kvq_t<f16, 32>(p, s);
             case 64: return launch_kvq_t<f16, 64>(p, s);
             case 128: return launch_kvq_t<f16, 128>(p, s);
+            case 256: return launch_kvq_t<f16, 256>(p, s);
         }
     } else {
         switch (D) {
@@ -90,6 +97,7 @@ hipError_t launch_bwd_kvq(const BwdParams &p, int dtype, int D, hipStream_t s) {
             case 32: return launch_kvq_t<float, 32>(p, s);
             case 64: return launch_kvq_t<float, 64>(p, s);
             case 128: return launch_kvq_t<float, 128>(p, s);
+            case 256: return launch_kvq_t<float, 256>(p, s);
         }
     }
     return hipErrorInvalidValue;

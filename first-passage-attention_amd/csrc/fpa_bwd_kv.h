@@ -3,7 +3,8 @@
 // Reference behaviour: _bwd_kv (kernel.py:177-265) of yliu-fort/first-passage-attention.
 // gfx950 design: a workgroup of FPA_NW waves owns
 // 32 keys per wave (one key per lane column) and streams 64-query blocks from the
-// diagonal to T through double-buffered, padded LDS tiles filled by direct global->LDS
+// diagonal to T through double-buffered (single-buffered where two stages do not fit in LDS:
+// fp32 at D = 256), padded LDS tiles filled by direct global->LDS
 // loads (one barrier per block).  Each wave computes S = Q K^T and dP = dO V^T with K, V
 // held in registers, then dV^T += dO^T P and dK^T += Q^T dS on the 32x32 MFMA (dO^T
 // and Q^T read from the row-major tiles with LDS transpose reads).  Per key it reduces
@@ -46,22 +47,33 @@ __device__ __forceinline__ float beta_eff(float betal) { return betal != 0.f ? b
 template <typename T, int D>
 constexpr int kv_wpe() { return (D >= 128 || (sizeof(T) == 4 && D >= 64)) ? 1 : FPA_KV_WPE; }
 
+// Parts of the head dimension whose dK / dV accumulators one workgroup holds: at D = 256 the
+// accumulators and the K, V rows together exceed the registers of a wave, so each key tile is
+// run twice (four times in fp32), each run accumulating dK and dV over one part of D and
+// recomputing S and dP; the per-key scalars (dpsi, dbeta, W, TBUF, GD) come from part 0.
+template <typename T, int D>
+constexpr int kv_parts() { return D >= 256 ? (sizeof(T) == 2 ? 2 : 4) : 1; }
+
 // LDS of one key-side workgroup.
 template <typename T, int D, int NW>
 struct KvShared {
     static constexpr int TB = Pad<T, (D < 32 ? 32 : D)>::template bytes<64>();  // one padded Q or dO tile
-    __attribute__((aligned(1024))) char Qs[2][TB];
-    __attribute__((aligned(1024))) char dOs[2][TB];
-    __attribute__((aligned(1024))) float qi[2][QI_PLANES][64];  // per-query values of a block: LQ, DL, PRE, ZQ, BST
+    static constexpr int NS = tile_stages<TB>(2 * QI_PLANES * 64 * 4 + 32 * NW * 4);
+    __attribute__((aligned(1024))) char Qs[NS][TB];
+    __attribute__((aligned(1024))) char dOs[NS][TB];
+    __attribute__((aligned(1024))) float qi[NS][QI_PLANES][64];  // per-query values of a block: LQ, DL, PRE, ZQ, BST
     __attribute__((aligned(16))) float kPHI[32 * NW];
 };
 
 // Keys [32 NW kt, 32 NW (kt + 1)) of head bh: every query block from the keys' diagonal block to T.
 template <typename T, int D, int NW>
-__device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, NW> &sm, const int kt, const int bh) {
+__device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, NW> &sm, const int kt, const int bh,
+                                            const int part = 0) {
     constexpr int BK = 32 * NW, BQ = 64;   // keys per workgroup, queries per iteration (one block)
     constexpr int DT = D < 32 ? 32 : D;
-    constexpr int NDT = DT / 32;
+    constexpr int NDT = DT / 32 / kv_parts<T, D>();  // dK / dV column tiles of this part
+    const int dt0 = part * NDT;
+    const bool scalars = part == 0;  // this run writes the per-key scalars
     auto &Qs = sm.Qs;
     auto &dOs = sm.dOs;
     auto &qi = sm.qi;
@@ -84,7 +96,7 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
     const T *DOb = static_cast<const T *>(p.dout) + b * p.sdo.b + h * p.sdo.h;
     // A block's per-query values: planes 0-3 (LQ, DL, PRE, ZQ) and 4-7 (BST, three unused) with one
     // 1 KB load each, from the even and the odd waves (no wave-dependent branch).  After the last
-    // block the prefetch repeats it into the other buffer, which is not read again.
+    // block the prefetch repeats it into a buffer that is not read again.
     const float *qi_head = p.qinfo + qi_at(bh, p.NB, 0, 0);
 
     TileLoader<T, D, DT, BQ, NW> qld, dld;
@@ -150,9 +162,10 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
     float rs = Cs, sv = (Cs > ninf()) ? fexp2(sufl - Cs) : 0.f;
     wait_loads();
     __syncthreads();
+    constexpr int NS = KvShared<T, D, NW>::NS;
     for (int ib = ib0, it = 0; ib < p.NB; ++ib, ++it) {
-        const int buf = it & 1;
-        issue(umin_i(ib + 1, p.NB - 1), buf ^ 1);
+        const int buf = (NS == 2) ? (it & 1) : 0;
+        if constexpr (NS == 2) issue(umin_i(ib + 1, p.NB - 1), buf ^ 1);
         const float bm_here = qi[buf][QI_BST][0], bl_cur = qi[buf][QI_BST][1];  // block ib
         if (wave_active && ib >= jb) {
             // Soft-min denominators off the diagonal: Z_ts 2^{-rs} = sv + 2^{PREL_t - rs} with the
@@ -183,8 +196,9 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
             for (int mt = 0; mt < 2; ++mt) {
                 f32x16 S, dP;
                 // S - lse / sc2 and dP - Delta, rows t, columns s
-                S = mma_p1_pad_reg<T, D, DT>(rows16(qi[buf][QI_LQ], mt), Qt, 32 * mt + c, g, kreg);
-                dP = mma_p1_pad_reg<T, D, DT>(rows16(qi[buf][QI_DL], mt), Dt, 32 * mt + c, g, vreg);
+                S = rows16(qi[buf][QI_LQ], mt);
+                dP = rows16(qi[buf][QI_DL], mt);
+                mma_p1_pad_reg2<T, D, DT>(S, Qt, 32 * mt + c, kreg, dP, Dt, 32 * mt + c, vreg, g);
                 float X[16];
                 if (diag) diag_x_queries(X, r, phiblk, mt, sr, g);  // X_ts = min phi(s, t] in the block
                 if (!diag) {
@@ -240,21 +254,21 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
                             S[j] = P;
                             dP[j] = dS;
                         }
-                        if (s_valid) *reinterpret_cast<f32x4 *>(p.gd + ((brow + jb) * G + sr) * G + t4) = g4;
+                        if (s_valid && scalars) *reinterpret_cast<f32x4 *>(p.gd + ((brow + jb) * G + sr) * G + t4) = g4;
                     }
                 }
                 // dV^T[d][s] += dO^T[d][t] P[t][s];  dK^T[d][s] += Q^T[d][t] dS[t][s]
 #pragma unroll
                 for (int dt = 0; dt < NDT; ++dt) {
-                    dvacc[dt] = mma_p2_p3_pad<T, DT, true>(dvacc[dt], S, Dt, 32 * mt, 32 * dt, lane);
-                    dkacc[dt] = mma_p2_p3_pad<T, DT, true>(dkacc[dt], dP, Qt, 32 * mt, 32 * dt, lane);
+                    dvacc[dt] = mma_p2_p3_pad<T, DT, true>(dvacc[dt], S, Dt, 32 * mt, 32 * (dt0 + dt), lane);
+                    dkacc[dt] = mma_p2_p3_pad<T, DT, true>(dkacc[dt], dP, Qt, 32 * mt, 32 * (dt0 + dt), lane);
                 }
             }
             if (ib > jb) {  // close query block ib: key-block and middle-block soft-min sums
                 if (rs > ninf()) Wacc = fmaf(fexp2(Cs - rs), wblk, Wacc);
                 if (ib > jb + 1) {
                     const float tp = wave_sum((rs > ninf()) ? fexp2(cmid - rs) * wblk : 0.f);
-                    if (lane == 0) p.tbuf[((brow + ib) * p.NB + jb) * 2 + ((kw0 / 32) & 1)] = tp;
+                    if (lane == 0 && scalars) p.tbuf[((brow + ib) * p.NB + jb) * 2 + ((kw0 / 32) & 1)] = tp;
                 }
             }
         }
@@ -265,6 +279,10 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
             rs = fmaxf(Cs, cmid);
             sv = (rs > ninf()) ? fexp2(sufl - rs) + fexp2(midl - rs) : 0.f;
         }
+        if constexpr (NS == 1) {  // every wave is done with the tiles: load the next block in their place
+            __syncthreads();
+            issue(umin_i(ib + 1, p.NB - 1), 0);
+        }
         wait_loads();
         __syncthreads();
     }
@@ -274,9 +292,11 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
     Wacc = sum_halves(Wacc);
     const float dbw = wave_sum(dbacc) / beff;
     if (!wave_active) return;
-    if (lane == 0) p.dbp[(int64_t)bh * p.NK32 + kw0 / 32] = dbw;  // one partial per 32-key group
-    if (g == 0 && s < p.TP) p.wsum[rowbase + s] = Wacc;
-    if (g == 0 && s_valid) p.dpsi[(int64_t)bh * p.T + s] = -beta * gsum;
+    if (scalars) {
+        if (lane == 0) p.dbp[(int64_t)bh * p.NK32 + kw0 / 32] = dbw;  // one partial per 32-key group
+        if (g == 0 && s < p.TP) p.wsum[rowbase + s] = Wacc;
+        if (g == 0 && s_valid) p.dpsi[(int64_t)bh * p.T + s] = -beta * gsum;
+    }
     if (!s_valid) return;
     T *dKr = static_cast<T *>(p.dk) + b * p.sdk.b + h * p.sdk.h + (int64_t)s * p.sdk.t;
     T *dVr = static_cast<T *>(p.dv) + b * p.sdv.b + h * p.sdv.h + (int64_t)s * p.sdv.t;
@@ -284,7 +304,7 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
         for (int jq = 0; jq < 4; ++jq) {
-            const int d0 = 32 * dt + 8 * jq + 4 * g;
+            const int d0 = 32 * (dt0 + dt) + 8 * jq + 4 * g;
             if (d0 < D) {
                 if constexpr (sizeof(T) == 2) {
                     h4 kv4 = {(f16)(dkacc[dt][4 * jq + 0] * p.smscale), (f16)(dkacc[dt][4 * jq + 1] * p.smscale),

@@ -10,7 +10,7 @@ template <typename T, int D>
 __global__ void __launch_bounds__(NTHREADS) fpa_bwd_prep_kernel(BwdParams p) {
     constexpr int CE = MT<T>::CHUNK;
     constexpr int CPR = (D + CE - 1) / CE;
-    const int bh = group_y(), b = bh / p.H, h = bh % p.H;
+    const int bh = group_bh(p.H), b = bh / p.H, h = bh % p.H;
     const int row = group_x() * 64 + thread_x() / 4, part = thread_x() % 4;
     float acc = 0.f;
     if (row < p.T) {
@@ -53,22 +53,23 @@ template <typename T, int D, int WPE, int NW>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 fpa_bwd_kv_kernel(BwdParams p) {
     __shared__ KvShared<T, D, NW> sm;
+    constexpr int NP = kv_parts<T, D>();
     int rank, bh;
-    xcd_work_item(rank, bh, p.BH, (p.T + 32 * NW - 1) / (32 * NW));
-    bwd_kv_tile<T, D, NW>(p, sm, rank, bh);  // rank 0: the heaviest key tile (most query blocks)
+    xcd_work_item(rank, bh, p.BH, p.H, NP * ((p.T + 32 * NW - 1) / (32 * NW)));
+    bwd_kv_tile<T, D, NW>(p, sm, rank / NP, bh, rank % NP);  // rank 0: the heaviest key tile (most query blocks)
 }
 
 template <typename T, int D>
 static hipError_t launch_prep_t(const BwdParams &p, hipStream_t s) {
-    hipLaunchKernelGGL((fpa_bwd_prep_kernel<T, D>), dim3(p.TP / 64, p.BH), dim3(NTHREADS), 0, s, p);
+    hipLaunchKernelGGL((fpa_bwd_prep_kernel<T, D>), head_grid(p.TP / 64, p.H, p.BH), dim3(NTHREADS), 0, s, p);
     return hipGetLastError();
 }
 
 template <typename T, int D>
 static hipError_t launch_kv_t(const BwdParams &p, hipStream_t s) {
     constexpr int NW = FPA_NW, WPE = kv_wpe<T, D>();
-    const int nkt = (p.T + 32 * NW - 1) / (32 * NW);
-    hipLaunchKernelGGL((fpa_bwd_kv_kernel<T, D, WPE, NW>), dim3(nkt, p.BH), dim3(64 * NW), 0, s, p);
+    const int nkt = kv_parts<T, D>() * ((p.T + 32 * NW - 1) / (32 * NW));
+    hipLaunchKernelGGL((fpa_bwd_kv_kernel<T, D, WPE, NW>), head_grid(nkt, p.H, p.BH), dim3(64 * NW), 0, s, p);
     return hipGetLastError();
 }
 
@@ -79,6 +80,7 @@ static hipError_t launch_kv_t(const BwdParams &p, hipStream_t s) {
             case 32: return FN<f16, 32>(p, s);             \
             case 64: return FN<f16, 64>(p, s);             \
             case 128: return FN<f16, 128>(p, s);           \
+            case 256: return FN<f16, 256>(p, s);           \
         }                                                  \
     } else {                                               \
         switch (D) {                                       \
@@ -86,6 +88,7 @@ static hipError_t launch_kv_t(const BwdParams &p, hipStream_t s) {
             case 32: return FN<float, 32>(p, s);           \
             case 64: return FN<float, 64>(p, s);           \
             case 128: return FN<float, 128>(p, s);         \
+            case 256: return FN<float, 256>(p, s);         \
         }                                                  \
     }                                                      \
     return hipErrorInvalidValue;

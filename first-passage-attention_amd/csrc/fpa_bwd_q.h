@@ -3,7 +3,8 @@
 // Reference behaviour: _bwd_q (kernel.py:286-340) of yliu-fort/first-passage-attention.
 // gfx950 design: a workgroup of FPA_NW waves owns 32 queries per wave (one query per lane
 // column) and streams 64-key blocks from the diagonal down to key 0 through
-// double-buffered, padded LDS tiles filled by direct global->LDS loads (one barrier per
+// double-buffered (single-buffered where two stages do not fit in LDS: fp32 at D = 256),
+// padded LDS tiles filled by direct global->LDS loads (one barrier per
 // block).  Each wave
 // recomputes S^T = K Q^T and dP^T = V dO^T with Q, dO in registers, accumulates
 // dQ^T += K^T dS^T on the 32x32 MFMA (K^T read from the row-major tile with LDS
@@ -36,12 +37,13 @@ constexpr int q_wpe() { return (D >= 128) ? 1 : FPA_Q_WPE; }
 template <typename T, int D, int NW>
 struct QShared {
     static constexpr int TB = Pad<T, (D < 32 ? 32 : D)>::template bytes<64>();  // one padded K or V tile
-    __attribute__((aligned(1024))) char Ks[2][TB];
-    __attribute__((aligned(1024))) char Vs[2][TB];
+    static constexpr int NS = tile_stages<TB>(2 * 8 * 64 * 4 + NW * 64 * 4);
+    __attribute__((aligned(1024))) char Ks[NS][TB];
+    __attribute__((aligned(1024))) char Vs[NS][TB];
     // Per-key values of a block: BSUF, CP (= betal * psi), SUFL, PHI, and BST (BMIN, BLSE, SUF of the
     // first key at [4][0..2]; planes 4-7 are four copies, so the two halves are one 1 KB load each
     // from the even and the odd waves).
-    __attribute__((aligned(1024))) float kst[2][8][64];
+    __attribute__((aligned(1024))) float kst[NS][8][64];
     __attribute__((aligned(16))) float Aw[NW][64];  // per-wave key factors of the shared-reference path
 };
 
@@ -130,10 +132,11 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
     float bm_prev = 0.f, bl_prev = 0.f;
     wait_loads();
     __syncthreads();
+    constexpr int NS = QShared<T, D, NW>::NS;
     for (int jb = jbmax, it = 0; jb >= 0; --jb, ++it) {
-        const int buf = it & 1;
+        const int buf = (NS == 2) ? (it & 1) : 0;
         const int s0 = jb * BK;
-        issue(jb > 0 ? jb - 1 : 0, buf ^ 1);
+        if constexpr (NS == 2) issue(jb > 0 ? jb - 1 : 0, buf ^ 1);
         const float bm_here = kst[buf][4][0], bl_here = kst[buf][4][1], suf_first = kst[buf][4][2];
         if (wave_active && jb <= ib) {
             const float *kSUF = kst[buf][0], *kPSI = kst[buf][1], *kSUFL = kst[buf][2], *kPHI = kst[buf][3];
@@ -165,8 +168,8 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
 #pragma unroll 1
             for (int mt = 1; mt >= 0; --mt) {
                 // S' = S - lse_t / sc2 and dP' = dP - Delta_t  ([s][t])
-                f32x16 S = mma_p1_pad_reg<T, D, DT>(lq16, Kt, 32 * mt + c, g, qreg);
-                f32x16 dP = mma_p1_pad_reg<T, D, DT>(dl16, Vt, 32 * mt + c, g, doreg);
+                f32x16 S = lq16, dP = dl16;
+                mma_p1_pad_reg2<T, D, DT>(S, Kt, 32 * mt + c, qreg, dP, Vt, 32 * mt + c, doreg, g);
                 float X[16];
                 if (diag) diag_x_keys(X, r, kPHI, mt, tr, g);  // X_ts = min phi(s, t] in the block
                 if (!diag) {
@@ -230,6 +233,10 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
         }
         bm_prev = bm_here;
         bl_prev = bl_here;
+        if constexpr (NS == 1) {  // every wave is done with the tiles: load the next block in their place
+            __syncthreads();
+            issue(jb > 0 ? jb - 1 : 0, 0);
+        }
         wait_loads();
         __syncthreads();
     }

@@ -12,7 +12,7 @@ fpa_bwd_q_kernel(BwdParams p) {
     __shared__ QShared<T, D, NW> sm;
     const int nqt = (p.T + 32 * NW - 1) / (32 * NW);
     int rank, bh;
-    xcd_work_item(rank, bh, p.BH, nqt);
+    xcd_work_item(rank, bh, p.BH, p.H, nqt);
     bwd_q_tile<T, D, NW>(p, sm, nqt - 1 - rank, bh);  // rank 0: the longest rows
 }
 
@@ -21,7 +21,7 @@ static hipError_t launch_q_t(const BwdParams &p, hipStream_t s) {
     constexpr int NW = FPA_NW;
     const int nqt = (p.T + 32 * NW - 1) / (32 * NW);
     constexpr int WPE = q_wpe<T, D>();
-    hipLaunchKernelGGL((fpa_bwd_q_kernel<T, D, WPE, NW>), dim3(nqt, p.BH), dim3(64 * NW), 0, s, p);
+    hipLaunchKernelGGL((fpa_bwd_q_kernel<T, D, WPE, NW>), head_grid(nqt, p.H, p.BH), dim3(64 * NW), 0, s, p);
     return hipGetLastError();
 }
 
@@ -32,6 +32,7 @@ hipError_t launch_bwd_q(const BwdParams &p, int dtype, int D, hipStream_t s) {
             case 32: return launch_q_t<f16, 32>(p, s);
             case 64: return launch_q_t<f16, 64>(p, s);
             case 128: return launch_q_t<f16, 128>(p, s);
+            case 256: return launch_q_t<f16, 256>(p, s);
         }
     } else {
         switch (D) {
@@ -39,6 +40,7 @@ hipError_t launch_bwd_q(const BwdParams &p, int dtype, int D, hipStream_t s) {
             case 32: return launch_q_t<float, 32>(p, s);
             case 64: return launch_q_t<float, 64>(p, s);
             case 128: return launch_q_t<float, 128>(p, s);
+            case 256: return launch_q_t<float, 256>(p, s);
         }
     }
     return hipErrorInvalidValue;

@@ -320,6 +320,11 @@ template <typename T, int DT> struct Pad {
     template <int NR> static constexpr int bytes() { return NR * ROWB; }
 };
 
+// LDS stages of a pair of padded tiles streamed through a block loop: two (the next block's loads
+// are issued before this block's work) when two pairs and `extra` bytes fit in the 160 KB of a
+// CU, else one (the loads of the next block follow this block's work).
+template <int TB> constexpr int tile_stages(int extra) { return (4 * TB + extra <= 160 * 1024) ? 2 : 1; }
+
 // Raw buffer resource (four SGPRs) over bytes [base, base + 2^31) of a wave-uniform pointer:
 // base address (48 bits, stride 0), number of records, and the format word.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -422,6 +427,34 @@ __device__ __forceinline__ f32x16 mma_p1_pad_reg(f32x16 acc, const char *tile, i
     return mma_p1_lds_reg<T, K>(acc, reinterpret_cast<const T *>(tile) + row * Pad<T, DT>::PITCH, g, breg);
 }
 
+// Two independent mma_p1_pad_reg chains with their steps alternated, so that each MFMA's
+// accumulator dependency is covered by the other chain's MFMA instead of a stall.
+template <typename T, int K, int DT>
+__device__ __forceinline__ void mma_p1_pad_reg2(f32x16 &accA, const char *tileA, int rowA, const OpRow<T, K> &bA,
+                                                f32x16 &accB, const char *tileB, int rowB, const OpRow<T, K> &bB,
+                                                int g) {
+    const T *ra = reinterpret_cast<const T *>(tileA) + rowA * Pad<T, DT>::PITCH;
+    const T *rb = reinterpret_cast<const T *>(tileB) + rowB * Pad<T, DT>::PITCH;
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+        for (int i = 0; i < K / 16; ++i) {
+            accA = MT<T>::mma(*reinterpret_cast<const h8 *>(ra + 16 * i + 8 * g), bA[i], accA);
+            accB = MT<T>::mma(*reinterpret_cast<const h8 *>(rb + 16 * i + 8 * g), bB[i], accB);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < K / 8; ++i) {
+            const f32x4 a = *reinterpret_cast<const f32x4 *>(ra + g * (K / 2) + 4 * i);
+            const f32x4 b = *reinterpret_cast<const f32x4 *>(rb + g * (K / 2) + 4 * i);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                accA = MT<T>::mma(a[e], bA[4 * i + e], accA);
+                accB = MT<T>::mma(b[e], bB[4 * i + e], accB);
+            }
+        }
+    }
+}
+
 // fp16 form of mma_p2_p3_pad with the P2 operand already converted: p2[hf] holds registers
 // 8 * hf .. 8 * hf + 7 of the accumulator tile.
 template <int DT, bool A_IS_P3>
@@ -463,20 +496,27 @@ __device__ __forceinline__ void load_row_p1(OpRow<T, D> &dst, const T *rowp, boo
 __device__ __forceinline__ int thread_x() { return __builtin_amdgcn_workitem_id_x(); }
 __device__ __forceinline__ int group_x() { return __builtin_amdgcn_workgroup_id_x(); }
 __device__ __forceinline__ int group_y() { return __builtin_amdgcn_workgroup_id_y(); }
+__device__ __forceinline__ int group_z() { return __builtin_amdgcn_workgroup_id_z(); }
 
-// Work item of this workgroup in a grid of (ntiles, BH): rank 0 is the heaviest tile.
-// Workgroups are dispatched in linear order, round-robin over the 8 XCDs of the chip; when
-// BH is a multiple of 8 every head is pinned to one XCD (its K/V stay in that XCD's L2)
-// and each XCD takes its heads' tiles heaviest first.
-__device__ __forceinline__ void xcd_work_item(int &rank, int &bh, int BH, int ntiles) {
-    const int L = group_x() + ntiles * group_y();
+// Per-head grids are (n, H, B), as many workgroups per head as the kernel needs times H times
+// B (each at most 65535, the grid's y and z limits); the flattened head index is b * H + h.
+__device__ __forceinline__ int group_bh(int H) { return group_z() * H + group_y(); }
+inline dim3 head_grid(int n, int H, int BH) { return dim3(n, H, BH / H); }
+
+// Work item of this workgroup in a per-head grid of ntiles workgroups per head: rank 0 is the
+// heaviest tile.  Workgroups are dispatched in linear order (x fastest, then the head), round-
+// robin over the 8 XCDs of the chip; when BH is a multiple of 8 every head is pinned to one XCD
+// (its K/V stay in that XCD's L2) and each XCD takes its heads' tiles heaviest first.  The
+// entry points keep ntiles * BH below 2^31.
+__device__ __forceinline__ void xcd_work_item(int &rank, int &bh, int BH, int H, int ntiles) {
+    const int L = group_x() + ntiles * group_bh(H);
     if ((BH & 7) == 0) {
         const int xcd = L & 7, k = L >> 3, hpx = BH >> 3;
         rank = k / hpx;
         bh = (k % hpx) * 8 + xcd;
     } else {
         rank = group_x();
-        bh = group_y();
+        bh = group_bh(H);
     }
     rank = __builtin_amdgcn_readfirstlane(rank);  // uniform: loop bounds and addresses stay scalar
     bh = __builtin_amdgcn_readfirstlane(bh);

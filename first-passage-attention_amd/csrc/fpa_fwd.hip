@@ -5,8 +5,9 @@
 //   * statistics: one wave per block of G = 64 positions, prefix/suffix min and
 //     base-2 log-sum-exp by wave shuffles;
 //   * forward: a workgroup of FPA_NW waves owns 32 query rows per wave, streams
-//     64-key tiles from the diagonal down to key 0 through double-buffered, padded
-//     LDS tiles filled by direct global->LDS loads (one barrier per tile), computes
+//     64-key tiles from the diagonal down to key 0 through double-buffered (single-
+//     buffered for fp32 at D = 256, where two stages do not fit in LDS), padded LDS
+//     tiles filled by direct global->LDS loads (one barrier per tile), computes
 //     S^T = K Q^T and O^T += V^T P^T on the 32x32 MFMA (V^T read from the row-major
 //     tile with LDS transpose reads), and keeps each query's online-softmax state in
 //     its own lane.
@@ -35,7 +36,7 @@ namespace fpa {
 //   BSUF      : beta*log2e*SUF (the query side's per-key term)
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(64) fpa_stats_kernel(StatsParams p) {
-    const int blk = group_x(), bh = group_y();
+    const int blk = group_x(), bh = group_bh(p.H);
     const int b = bh / p.H, h = bh % p.H;
     const int lane = thread_x();
     const int u = blk * G + lane;
@@ -91,7 +92,7 @@ __global__ void __launch_bounds__(64) fpa_stats_kernel(StatsParams p) {
 }
 
 hipError_t launch_stats(const StatsParams &p, hipStream_t s) {
-    hipLaunchKernelGGL(fpa_stats_kernel, dim3(p.NB, p.BH), dim3(64), 0, s, p);
+    hipLaunchKernelGGL(fpa_stats_kernel, head_grid(p.NB, p.H, p.BH), dim3(64), 0, s, p);
     return hipGetLastError();
 }
 
@@ -117,16 +118,17 @@ fpa_fwd_kernel(FwdParams p) {
     constexpr int DT = D < 32 ? 32 : D;
     constexpr int NDT = DT / 32;
     constexpr int TB = Pad<T, DT>::template bytes<BN>();  // one padded K or V tile
-    __shared__ __attribute__((aligned(1024))) char Ks[2][TB];
-    __shared__ __attribute__((aligned(1024))) char Vs[2][TB];
+    constexpr int NS = tile_stages<TB>(2 * 4 * BN * 4);
+    __shared__ __attribute__((aligned(1024))) char Ks[NS][TB];
+    __shared__ __attribute__((aligned(1024))) char Vs[NS][TB];
     // Per-key values of a tile: CA, CP, PHI and BST (the block's BMIN at [3][0]).
-    __shared__ __attribute__((aligned(1024))) float cst[2][4][BN];
+    __shared__ __attribute__((aligned(1024))) float cst[NS][4][BN];
 
     const int tid = thread_x(), lane = tid % 64, g = lane / 32, c = lane % 32;
     const int w = __builtin_amdgcn_readfirstlane(tid / 64);  // wave index, uniform across the wave
     const int nqt = (p.T + BM - 1) / BM;
     int rank, bh;
-    xcd_work_item(rank, bh, p.BH, nqt);
+    xcd_work_item(rank, bh, p.BH, p.H, nqt);
     const int qt = nqt - 1 - rank;  // longest rows first
     const int b = bh / p.H, h = bh % p.H;
     const int q0 = qt * BM, qw0 = q0 + 32 * w, tq = qw0 + c;
@@ -145,7 +147,7 @@ fpa_fwd_kernel(FwdParams p) {
 
     // Tile jt of K, V and the per-key values into buffer `buf` (shared out over the waves; every wave
     // issues the per-key load, identical writes instead of a wave-dependent branch).  After tile 0
-    // the prefetch repeats it into the other buffer, which is not read again.
+    // the prefetch repeats it into a buffer that is not read again.
     TileLoader<T, D, DT, BN, NW> kld, vld;
     kld.init(p.sk.t, w, lane);
     vld.init(p.sv.t, w, lane);
@@ -176,9 +178,9 @@ fpa_fwd_kernel(FwdParams p) {
     wait_loads();
     __syncthreads();
     for (int jt = jtmax, it = 0; jt >= 0; --jt, ++it) {
-        const int buf = it & 1;
+        const int buf = (NS == 2) ? (it & 1) : 0;
         const int s0 = jt * BN;
-        issue(jt > 0 ? jt - 1 : 0, buf ^ 1);
+        if constexpr (NS == 2) issue(jt > 0 ? jt - 1 : 0, buf ^ 1);
         if (wave_active && s0 <= qw0 + 31) {
             const char *Kt = Ks[buf];
             const float *cA = cst[buf][0], *cP = cst[buf][1], *cPHI = cst[buf][2];
@@ -190,8 +192,9 @@ fpa_fwd_kernel(FwdParams p) {
             // Both 32-key halves' scores first; then each half in turn (the second half's MFMAs
             // and the first half's P V run while the other half's VALU work goes on).
             f32x16 s[2];
-            s[1] = mma_p1_pad_reg<T, D, DT>(zero16(), Kt, 32 + c, g, qreg);
-            s[0] = mma_p1_pad_reg<T, D, DT>(zero16(), Kt, c, g, qreg);
+            s[0] = zero16();
+            s[1] = zero16();
+            mma_p1_pad_reg2<T, D, DT>(s[1], Kt, 32 + c, qreg, s[0], Kt, c, qreg, g);
 #pragma unroll
             for (int mt = 1; mt >= 0; --mt) {
                 if (!diag) {
@@ -278,6 +281,10 @@ fpa_fwd_kernel(FwdParams p) {
 
             if (jb < ib) mid = fminf(mid, cst[buf][3][0]);  // BMIN of block jb
         }
+        if constexpr (NS == 1) {  // every wave is done with the tile: load the next one in its place
+            __syncthreads();
+            issue(jt > 0 ? jt - 1 : 0, 0);
+        }
         wait_loads();
         __syncthreads();
     }
@@ -311,7 +318,7 @@ template <typename T, int D>
 static hipError_t launch_fwd_t(const FwdParams &p, hipStream_t s) {
     constexpr int NW = FPA_NW, WPE = (D >= 128) ? 1 : (sizeof(T) == 2 ? FPA_FWD_WPE : FPA_FWD_WPE32);
     const int nqt = (p.T + 32 * NW - 1) / (32 * NW);
-    hipLaunchKernelGGL((fpa_fwd_kernel<T, D, WPE, NW>), dim3(nqt, p.BH), dim3(64 * NW), 0, s, p);
+    hipLaunchKernelGGL((fpa_fwd_kernel<T, D, WPE, NW>), head_grid(nqt, p.H, p.BH), dim3(64 * NW), 0, s, p);
     return hipGetLastError();
 }
 
@@ -322,6 +329,7 @@ hipError_t launch_fwd(const FwdParams &p, int dtype, int D, hipStream_t s) {
             case 32: return launch_fwd_t<f16, 32>(p, s);
             case 64: return launch_fwd_t<f16, 64>(p, s);
             case 128: return launch_fwd_t<f16, 128>(p, s);
+            case 256: return launch_fwd_t<f16, 256>(p, s);
         }
     } else {
         switch (D) {
@@ -329,6 +337,7 @@ hipError_t launch_fwd(const FwdParams &p, int dtype, int D, hipStream_t s) {
             case 32: return launch_fwd_t<float, 32>(p, s);
             case 64: return launch_fwd_t<float, 64>(p, s);
             case 128: return launch_fwd_t<float, 128>(p, s);
+            case 256: return launch_fwd_t<float, 256>(p, s);
         }
     }
     return hipErrorInvalidValue;

@@ -96,7 +96,10 @@ hipError_t launch_field_bwd(const FieldParams &p, int dtype, hipStream_t s);
 // Head dimensions with built kernels.
 inline bool supported_d(int dtype, int D) {
     (void)dtype;
-    return D == 16 || D == 32 || D == 64 || D == 128;
+    return D == 16 || D == 32 || D == 64 || D == 128 || D == 256;
 }
+
+// Most 64-blocks of T (the combine kernel stages three floats per block in LDS): T <= 524288.
+constexpr int MAX_NB = 8192;
 
 }  // namespace fpa
