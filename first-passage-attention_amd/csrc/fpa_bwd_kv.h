@@ -28,6 +28,10 @@
 #ifndef FPA_KV_PROD
 #define FPA_KV_PROD 1
 #endif
+// Per-key fast paths of off-diagonal blocks (see bwd_kv_tile); 0 turns them off.
+#ifndef FPA_KV_CLASSES
+#define FPA_KV_CLASSES 1
+#endif
 
 namespace fpa {
 
@@ -192,6 +196,16 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
             const int sr = s - sb;
             float r = pinf();  // running min of phi over (s, u] for the in-block scan
             float wblk = 0.f;
+            // Off the diagonal, when every query of block ib has PRE_t >= m_s = min(SUF_s, MID) for
+            // every key of the wave (the block's minimum BMIN >= m_s), x_ts = m_s - psi_s for all t:
+            // the bias is cAz per key and the gate m_s <= psi_s is per key, so the block needs only
+            // sum_t dS_ts per key (class 1).  When moreover 2^{BLSE - rs} <= 2^-25 for every key, each
+            // Z_ts 2^{-rs} = sv + 2^{PREL_t - rs} equals sv to within 2^-25 (sv >= 1), below fp32
+            // resolution: the soft-min sum is sum_t g_ts / sv (class 2).
+            int cls = 0;
+            if (FPA_KV_CLASSES && !diag && __all(bm_here >= fminf(suf, mid)))
+                cls = __all(bl_cur - rs <= -25.f) ? 2 : 1;
+            float dsum = 0.f;  // classes 1, 2: sum of dS over the block
 #pragma unroll 1
             for (int mt = 0; mt < 2; ++mt) {
                 f32x16 S, dP;
@@ -204,8 +218,9 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
                 if (!diag) {
                     // Off the diagonal block every key is valid and every query is later than
                     // every key; rows of a ragged last block are past T and have P = 0.
-                    auto offdiag = [&](auto prod_c) {
+                    auto offdiag = [&](auto prod_c, auto cls_c) {
                         constexpr bool PROD = decltype(prod_c)::value;
+                        constexpr int CLS = decltype(cls_c)::value;
                         const float *rZQ = qi[buf][QI_ZQ];
 #pragma unroll
                         for (int jq = 0; jq < 4; ++jq) {
@@ -215,23 +230,40 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
 #pragma unroll
                             for (int e = 0; e < 4; ++e) {
                                 const int j = 4 * jq + e;
-                                const float bm = __builtin_amdgcn_fmed3f(fmaf(pre4[e], beff, nbpsi), cAz, E);
-                                const float P = fexp2(fmaf(S[j], p.sc2, bm));
-                                const float dS = P * dP[j];
-                                const float gg = (pre4[e] <= thr) ? dS : 0.f;
-                                gsum += gg;
-                                dbacc = fmaf(dS, bm, dbacc);
-                                const float z = PROD ? fmaf(zq4[e], ck, sv) : sv + fexp2(zq4[e] - rsb);
-                                wblk = fmaf(gg, frcp(z), wblk);
-                                S[j] = P;
-                                dP[j] = dS;
+                                if constexpr (CLS == 0) {
+                                    const float bm = __builtin_amdgcn_fmed3f(fmaf(pre4[e], beff, nbpsi), cAz, E);
+                                    const float P = fexp2(fmaf(S[j], p.sc2, bm));
+                                    const float dS = P * dP[j];
+                                    const float gg = (pre4[e] <= thr) ? dS : 0.f;
+                                    gsum += gg;
+                                    dbacc = fmaf(dS, bm, dbacc);
+                                    const float z = PROD ? fmaf(zq4[e], ck, sv) : sv + fexp2(zq4[e] - rsb);
+                                    wblk = fmaf(gg, frcp(z), wblk);
+                                    S[j] = P;
+                                    dP[j] = dS;
+                                } else {
+                                    const float P = fexp2(fmaf(S[j], p.sc2, cAz));
+                                    const float dS = P * dP[j];
+                                    dsum += dS;
+                                    if constexpr (CLS == 1) {
+                                        const float z = PROD ? fmaf(zq4[e], ck, sv) : sv + fexp2(zq4[e] - rsb);
+                                        wblk = fmaf(dS, frcp(z), wblk);
+                                    }
+                                    S[j] = P;
+                                    dP[j] = dS;
+                                }
                             }
                         }
                     };
-                    if (prod)
-                        offdiag(std::true_type{});
+                    using C0 = std::integral_constant<int, 0>;
+                    using C1 = std::integral_constant<int, 1>;
+                    using C2 = std::integral_constant<int, 2>;
+                    if (cls == 2)
+                        offdiag(std::true_type{}, C2{});
+                    else if (cls == 1)
+                        prod ? offdiag(std::true_type{}, C1{}) : offdiag(std::false_type{}, C1{});
                     else
-                        offdiag(std::false_type{});
+                        prod ? offdiag(std::true_type{}, C0{}) : offdiag(std::false_type{}, C0{});
                 } else {
 #pragma unroll
                     for (int jq = 0; jq < 4; ++jq) {
@@ -263,6 +295,12 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
                     dvacc[dt] = mma_p2_p3_pad<T, DT, true>(dvacc[dt], S, Dt, 32 * mt, 32 * (dt0 + dt), lane);
                     dkacc[dt] = mma_p2_p3_pad<T, DT, true>(dkacc[dt], dP, Qt, 32 * mt, 32 * (dt0 + dt), lane);
                 }
+            }
+            if (cls > 0) {  // the per-key sums of classes 1 and 2
+                const bool gate = fminf(suf, mid) <= psi_s;
+                gsum += gate ? dsum : 0.f;
+                dbacc = fmaf(dsum, cAz, dbacc);
+                wblk = !gate ? 0.f : (cls == 2) ? dsum / sv : wblk;
             }
             if (ib > jb) {  // close query block ib: key-block and middle-block soft-min sums
                 if (rs > ninf()) Wacc = fmaf(fexp2(Cs - rs), wblk, Wacc);

@@ -26,6 +26,10 @@
 #ifndef FPA_Q_FAST
 #define FPA_Q_FAST 1
 #endif
+// Per-key fast paths of off-diagonal blocks on the shared-reference path; 0 turns them off.
+#ifndef FPA_Q_CLASSES
+#define FPA_Q_CLASSES 1
+#endif
 
 namespace fpa {
 
@@ -45,6 +49,8 @@ struct QShared {
     // from the even and the odd waves).
     __attribute__((aligned(1024))) float kst[NS][8][64];
     __attribute__((aligned(16))) float Aw[NW][64];  // per-wave key factors of the shared-reference path
+    __attribute__((aligned(16))) float Bw[NW][64];  // per-wave per-key bias and gate of classes 1, 2
+    __attribute__((aligned(16))) float Gw[NW][64];
 };
 
 // Queries [32 NW qt, 32 NW (qt + 1)) of head bh: every key block from their diagonal block down to 0.
@@ -57,6 +63,8 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
     auto &Vs = sm.Vs;
     auto &kst = sm.kst;
     auto &Aw = sm.Aw;
+    auto &Bw = sm.Bw;
+    auto &Gw = sm.Gw;
 
     const int tid = thread_x(), lane = tid % 64, g = lane / 32, c = lane % 32;
     const int w = __builtin_amdgcn_readfirstlane(tid / 64);  // wave index, uniform across the wave
@@ -160,6 +168,21 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
             }
             float rblk = 0.f;  // sum of g / (Z 2^{-R}) over this key block (shared-reference path)
             const float bY = betal * fminf(pre, mid);
+            // Shared-reference path, when every query of the wave has PRE_t >= MID (the largest
+            // min(SUF_s, MID) of a block is MID: its last key has an empty suffix), x_ts =
+            // min(SUF_s, MID) - psi_s for all t: bias and gate are per key, tabled once per block
+            // in Bw / Gw (class 1).  When moreover 2^{PREL_t - MIDL} <= 2^-25 for every query,
+            // Z_ts 2^{-R} = Aw_s + bq_t equals Aw_s to within 2^-25 (Aw_s >= 2^{MIDL - R}): the
+            // reciprocal is per key too (class 2, 1 / Aw_s in Aw).
+            int cls = 0;
+            if (FPA_Q_CLASSES && fast && __all(!t_valid || pre >= mid)) {
+                cls = __all(!t_valid || prel - midl <= -25.f) ? 2 : 1;
+                const float v = __builtin_amdgcn_fmed3f(kSUF[lane], betal * mid, E) - kPSI[lane];
+                const float bmk = __builtin_amdgcn_fmed3f(v, 0.f, E);
+                Bw[w][lane] = bmk;
+                Gw[w][lane] = (bmk == v) ? 1.f : 0.f;
+                if (cls == 2) Aw[w][lane] = 1.f / Aw[w][lane];
+            }
             const bool diag = (jb == ib);
             const int tr = tq - s0;
             const char *Kt = Ks[buf];
@@ -174,15 +197,30 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
                 if (diag) diag_x_keys(X, r, kPHI, mt, tr, g);  // X_ts = min phi(s, t] in the block
                 if (!diag) {
                     // Off the diagonal block every key is valid and earlier than every query.
-                    auto offdiag = [&](auto fast_c) {
+                    auto offdiag = [&](auto fast_c, auto cls_c) {
                         constexpr bool FAST = decltype(fast_c)::value;
+                        constexpr int CLS = decltype(cls_c)::value;
 #pragma unroll
                         for (int jq = 0; jq < 4; ++jq) {
                             const int s4 = 32 * mt + 8 * jq + 4 * g;
-                            const f32x4 bsuf4 = *reinterpret_cast<const f32x4 *>(&kSUF[s4]);
-                            const f32x4 bpsi4 = *reinterpret_cast<const f32x4 *>(&kPSI[s4]);
                             const f32x4 zk4 = FAST ? *reinterpret_cast<const f32x4 *>(&Aw[w][s4])
                                                    : *reinterpret_cast<const f32x4 *>(&kSUFL[s4]);
+                            if constexpr (CLS > 0) {
+                                const f32x4 bm4 = *reinterpret_cast<const f32x4 *>(&Bw[w][s4]);
+                                const f32x4 gt4 = *reinterpret_cast<const f32x4 *>(&Gw[w][s4]);
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) {
+                                    const int j = 4 * jq + e;
+                                    const float P = fexp2(fmaf(S[j], p.sc2, bm4[e]));
+                                    const float dS = P * dP[j];
+                                    const float gg = dS * gt4[e];
+                                    rblk = fmaf(gg, (CLS == 2) ? zk4[e] : frcp(zk4[e] + bq), rblk);
+                                    S[j] = dS;
+                                }
+                                continue;
+                            }
+                            const f32x4 bsuf4 = *reinterpret_cast<const f32x4 *>(&kSUF[s4]);
+                            const f32x4 bpsi4 = *reinterpret_cast<const f32x4 *>(&kPSI[s4]);
 #pragma unroll
                             for (int e = 0; e < 4; ++e) {
                                 const int j = 4 * jq + e;
@@ -201,12 +239,17 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
                             }
                         }
                     };
+                    using C0 = std::integral_constant<int, 0>;
 #if FPA_Q_FAST
-                    if (fast)
-                        offdiag(std::true_type{});
+                    if (cls == 2)
+                        offdiag(std::true_type{}, std::integral_constant<int, 2>{});
+                    else if (cls == 1)
+                        offdiag(std::true_type{}, std::integral_constant<int, 1>{});
+                    else if (fast)
+                        offdiag(std::true_type{}, C0{});
                     else
 #endif
-                        offdiag(std::false_type{});
+                        offdiag(std::false_type{}, C0{});
                 } else {
 #pragma unroll
                     for (int jq = 0; jq < 4; ++jq) {

@@ -38,6 +38,30 @@ class FwdBuffers:
         self.state = torch.empty(L.fpa_state_floats(B, H, T), dtype=torch.float32, device=dev)
 
 
+# Backward scratch kept per (device, stream) and grown on demand: a backward's kernels run in
+# stream order, so the next backward on the same stream may reuse the same bytes.  Under HIP graph
+# capture a fresh tensor is taken instead (from the graph's private pool, alive as long as the
+# graph), so a later growth of the cache never frees memory that a captured graph still uses.
+_WS_CACHE = {}
+
+
+def workspace(dev, nbytes):
+    """A uint8 device tensor of at least nbytes for one backward call on the current stream."""
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), torch.cuda.current_stream(dev).cuda_stream)
+    ws = _WS_CACHE.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        _WS_CACHE[key] = ws
+    return ws
+
+
+def release_workspaces():
+    """Drop the cached backward scratch (torch's allocator gets the memory back)."""
+    _WS_CACHE.clear()
+
+
 class BwdBuffers:
     """Gradients and scratch of one backward call."""
 
@@ -54,8 +78,7 @@ class BwdBuffers:
         self.dphi = torch.empty((B, H, T), dtype=torch.float32, device=dev)
         self.dpsi = torch.empty_like(self.dphi)
         self.dbeta = torch.empty(H, dtype=torch.float32, device=dev)
-        self.ws = torch.empty(L.fpa_bwd_workspace_bytes(B, H, T, D, _lib.dtype_code(q.dtype)),
-                              dtype=torch.uint8, device=dev)
+        self.ws = workspace(dev, L.fpa_bwd_workspace_bytes(B, H, T, D, _lib.dtype_code(q.dtype)))
 
 
 def fwd_args(q, k, v, phi, psi, beta, tau, out):
