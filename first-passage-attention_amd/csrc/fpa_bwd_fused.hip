@@ -13,12 +13,13 @@
 #include "fpa_bwd_q.h"
 
 // Relative cost of one block iteration of the key side and of the query side, for the order
-// of the fused grid (measured alone at D = 64 fp16: 1.4; the fused launch is fastest with 1.5-2).
+// of the fused grid (measured alone at D = 64 fp16: about 1.2; the fused launch is fastest with
+// weights 5:4 to 6:5, 1% ahead of 3:2 and 4% ahead of 1:1 at cfg2, level at cfg4).
 #ifndef FPA_FUSE_WKV
-#define FPA_FUSE_WKV 3
+#define FPA_FUSE_WKV 5
 #endif
 #ifndef FPA_FUSE_WQ
-#define FPA_FUSE_WQ 2
+#define FPA_FUSE_WQ 4
 #endif
 
 namespace fpa {
