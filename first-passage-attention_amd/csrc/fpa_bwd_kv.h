@@ -193,6 +193,7 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
             const char *Dt = dOs[buf];
             const float *rPRE = qi[buf][QI_PRE];
             const bool diag = (ib == jb);
+            const bool upper = (kw0 - sb) >= 32;  // this wave holds keys 32-63 of its block
             const int sr = s - sb;
             float r = pinf();  // running min of phi over (s, u] for the in-block scan
             float wblk = 0.f;
@@ -207,14 +208,21 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
                 cls = __all(bl_cur - rs <= -25.f) ? 2 : 1;
             float dsum = 0.f;  // classes 1, 2: sum of dS over the block
 #pragma unroll 1
-            for (int mt = 0; mt < 2; ++mt) {
+            // On the diagonal the upper 32 keys come after every one of the first 32 queries: that
+            // quarter (all P = 0; its gd entries are never read) is skipped.
+            for (int mt = (diag && upper) ? 1 : 0; mt < 2; ++mt) {
                 f32x16 S, dP;
                 // S - lse / sc2 and dP - Delta, rows t, columns s
                 S = rows16(qi[buf][QI_LQ], mt);
                 dP = rows16(qi[buf][QI_DL], mt);
                 mma_p1_pad_reg2<T, D, DT>(S, Qt, 32 * mt + c, kreg, dP, Dt, 32 * mt + c, vreg, g);
                 float X[16];
-                if (diag) diag_x_queries(X, r, phiblk, mt, sr, g);  // X_ts = min phi(s, t] in the block
+                if (diag) {  // X_ts = min phi(s, t] in the block; the lower keys' second half is all after them
+                    if (mt == 1 && !upper)
+                        diag_x_queries<true>(X, r, phiblk, mt, sr, g);
+                    else
+                        diag_x_queries(X, r, phiblk, mt, sr, g);
+                }
                 if (!diag) {
                     // Off the diagonal block every key is valid and every query is later than
                     // every key; rows of a ragged last block are past T and have P = 0.
@@ -273,13 +281,14 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
                         for (int e = 0; e < 4; ++e) {
                             const int j = 4 * jq + e;
                             const int t = ib * BQ + t4 + e;
+                            // X is +inf where the range (s, t] is empty (t <= s): there x = +inf, the bias
+                            // beff * min(x, 0) is 0 and the gate x <= 0 is off, as for b_tt = 0.
                             const bool valid = (t >= s) && s_valid;  // rows past T have -inf scores: P = 0
-                            const bool strict = valid && (t > s);
                             const float x = X[j] - psi_s;
-                            const float bm = strict ? beff * fminf(x, 0.f) : 0.f;  // x is +inf where the range is empty
+                            const float bm = beff * fminf(x, 0.f);
                             const float P = valid ? fexp2(fmaf(S[j], p.sc2, bm)) : 0.f;
                             const float dS = P * dP[j];
-                            const float gg = (strict && x <= 0.f) ? dS : 0.f;
+                            const float gg = (x <= 0.f) ? dS : 0.f;
                             gsum += gg;
                             dbacc = fmaf(dS, bm, dbacc);
                             g4[e] = gg;

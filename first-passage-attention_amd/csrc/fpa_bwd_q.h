@@ -184,17 +184,25 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
                 if (cls == 2) Aw[w][lane] = 1.f / Aw[w][lane];
             }
             const bool diag = (jb == ib);
+            const bool upper = (qw0 - ib * G) >= 32;  // this wave holds queries 32-63 of its block
             const int tr = tq - s0;
             const char *Kt = Ks[buf];
             const char *Vt = Vs[buf];
             float r = pinf();  // running min of phi over [u, t] for the in-block scan
 #pragma unroll 1
-            for (int mt = 1; mt >= 0; --mt) {
+            // On the diagonal the upper 32 keys come after every one of the first 32 queries: that
+            // quarter (all P = 0) is skipped.
+            for (int mt = (diag && !upper) ? 0 : 1; mt >= 0; --mt) {
                 // S' = S - lse_t / sc2 and dP' = dP - Delta_t  ([s][t])
                 f32x16 S = lq16, dP = dl16;
                 mma_p1_pad_reg2<T, D, DT>(S, Kt, 32 * mt + c, qreg, dP, Vt, 32 * mt + c, doreg, g);
                 float X[16];
-                if (diag) diag_x_keys(X, r, kPHI, mt, tr, g);  // X_ts = min phi(s, t] in the block
+                if (diag) {  // X_ts = min phi(s, t] in the block; the upper queries' first half is all before them
+                    if (mt == 0 && upper)
+                        diag_x_keys<true>(X, r, kPHI, mt, tr, g);
+                    else
+                        diag_x_keys(X, r, kPHI, mt, tr, g);
+                }
                 if (!diag) {
                     // Off the diagonal block every key is valid and earlier than every query.
                     auto offdiag = [&](auto fast_c, auto cls_c) {

@@ -239,7 +239,9 @@ __device__ __forceinline__ f32x16 mma_p2_p3(f32x16 acc, const f32x16 (&c)[NT], c
 // scan; `r` carries min phi[32*mt + 33 .. tr] in and min phi[32*mt + 1 .. tr] out.  `phi` is
 // the block's 64 values in LDS (16-byte aligned): every read is unconditional (the same
 // address in all lanes) and positions past tr are masked by a select, so the scan has no
-// branches.
+// branches.  ALL_BEFORE: every key of the half is before every query of the wave (tr >= 32 * mt +
+// 32), no mask.
+template <bool ALL_BEFORE = false>
 __device__ __forceinline__ void diag_x_keys(float (&X)[16], float &r, const float *phi, int mt, int tr, int g) {
     float pv[33];
 #pragma unroll
@@ -252,7 +254,7 @@ __device__ __forceinline__ void diag_x_keys(float (&X)[16], float &r, const floa
 #pragma unroll
     for (int k = 32; k >= 1; --k) {
         const int u = 32 * mt + k;
-        r = fminf(r, (u <= tr) ? pv[k] : pinf());
+        r = fminf(r, (ALL_BEFORE || u <= tr) ? pv[k] : pinf());
         rr[k] = r;  // min phi[u .. tr]: the value for key u - 1
     }
 #pragma unroll
@@ -264,7 +266,9 @@ __device__ __forceinline__ void diag_x_keys(float (&X)[16], float &r, const floa
 
 // Lane = key sr (0..63 in the block); registers = queries 32*mt + acc_row(j, g).  Ascending
 // scan; `r` carries min phi[sr+1 .. 32*mt - 1] in and min phi[sr+1 .. 32*mt + 31] out.
-// Branch-free like diag_x_keys.
+// Branch-free like diag_x_keys.  ALL_AFTER: every query of the half is after every key of the
+// wave (sr < 32 * mt), no mask.
+template <bool ALL_AFTER = false>
 __device__ __forceinline__ void diag_x_queries(float (&X)[16], float &r, const float *phi, int mt, int sr, int g) {
     float pv[32];
 #pragma unroll
@@ -276,7 +280,7 @@ __device__ __forceinline__ void diag_x_queries(float (&X)[16], float &r, const f
 #pragma unroll
     for (int k = 0; k < 32; ++k) {
         const int u = 32 * mt + k;
-        r = fminf(r, (u > sr) ? pv[k] : pinf());
+        r = fminf(r, (ALL_AFTER || u > sr) ? pv[k] : pinf());
         rr[k] = r;  // min phi[sr+1 .. u]: the value for query u
     }
 #pragma unroll
