@@ -123,7 +123,7 @@ def cpu_baseline(cfg, seconds):
 
 def cpu_baseline_cfg1():
     """BASELINE.json config 1 (B1 H2 T256 D32 fp32, loss o.sum(), seed 0) forward+backward on the float32
-    CPU oracle: 3 warm-ups, median of 15 (the CPU-baseline plan of BASELINE.md)."""
+    CPU oracle: 3 warm-ups, median of 15."""
     import torch
     from oracle import fpa_oracle as O
     q, k, v, phi, psi, beta, do = make_inputs(CONFIGS["cfg1"], seed=0)
