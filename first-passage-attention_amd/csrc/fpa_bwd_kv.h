@@ -207,9 +207,9 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
             if (FPA_KV_CLASSES && !diag && __all(bm_here >= fminf(suf, mid)))
                 cls = __all(bl_cur - rs <= -25.f) ? 2 : 1;
             float dsum = 0.f;  // classes 1, 2: sum of dS over the block
-#pragma unroll 1
             // On the diagonal the upper 32 keys come after every one of the first 32 queries: that
             // quarter (all P = 0; its gd entries are never read) is skipped.
+#pragma unroll 1
             for (int mt = (diag && upper) ? 1 : 0; mt < 2; ++mt) {
                 f32x16 S, dP;
                 // S - lse / sc2 and dP - Delta, rows t, columns s

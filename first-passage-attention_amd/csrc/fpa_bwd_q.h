@@ -189,9 +189,9 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
             const char *Kt = Ks[buf];
             const char *Vt = Vs[buf];
             float r = pinf();  // running min of phi over [u, t] for the in-block scan
-#pragma unroll 1
             // On the diagonal the upper 32 keys come after every one of the first 32 queries: that
             // quarter (all P = 0) is skipped.
+#pragma unroll 1
             for (int mt = (diag && !upper) ? 0 : 1; mt >= 0; --mt) {
                 // S' = S - lse_t / sc2 and dP' = dP - Delta_t  ([s][t])
                 f32x16 S = lq16, dP = dl16;
