@@ -49,8 +49,7 @@ struct QShared {
     // from the even and the odd waves).
     __attribute__((aligned(1024))) float kst[NS][8][64];
     __attribute__((aligned(16))) float Aw[NW][64];  // per-wave key factors of the shared-reference path
-    __attribute__((aligned(16))) float Bw[NW][64];  // per-wave per-key bias and gate of classes 1, 2
-    __attribute__((aligned(16))) float Gw[NW][64];
+    __attribute__((aligned(16))) float Bw[NW][64];  // per-wave per-key bias of classes 1, 2
 };
 
 // Queries [32 NW qt, 32 NW (qt + 1)) of head bh: every key block from their diagonal block down to 0.
@@ -64,7 +63,6 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
     auto &kst = sm.kst;
     auto &Aw = sm.Aw;
     auto &Bw = sm.Bw;
-    auto &Gw = sm.Gw;
 
     const int tid = thread_x(), lane = tid % 64, g = lane / 32, c = lane % 32;
     const int w = __builtin_amdgcn_readfirstlane(tid / 64);  // wave index, uniform across the wave
@@ -171,17 +169,20 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
             // Shared-reference path, when every query of the wave has PRE_t >= MID (the largest
             // min(SUF_s, MID) of a block is MID: its last key has an empty suffix), x_ts =
             // min(SUF_s, MID) - psi_s for all t: bias and gate are per key, tabled once per block
-            // in Bw / Gw (class 1).  When moreover 2^{PREL_t - MIDL} <= 2^-25 for every query,
+            // in Bw (class 1).  When moreover 2^{PREL_t - MIDL} <= 2^-25 for every query,
             // Z_ts 2^{-R} = Aw_s + bq_t equals Aw_s to within 2^-25 (Aw_s >= 2^{MIDL - R}): the
-            // reciprocal is per key too (class 2, 1 / Aw_s in Aw).
+            // reciprocal is per key too (class 2, 1 / Aw_s in Aw).  The per-key gate goes into Aw:
+            // a closed gate makes the class-2 factor 0 and the class-1 denominator +inf (reciprocal
+            // 0), so g / Z is dS / Z with no per-element gate.
             int cls = 0;
             if (FPA_Q_CLASSES && fast && __all(!t_valid || pre >= mid)) {
                 cls = __all(!t_valid || prel - midl <= -25.f) ? 2 : 1;
                 const float v = __builtin_amdgcn_fmed3f(kSUF[lane], betal * mid, E) - kPSI[lane];
                 const float bmk = __builtin_amdgcn_fmed3f(v, 0.f, E);
                 Bw[w][lane] = bmk;
-                Gw[w][lane] = (bmk == v) ? 1.f : 0.f;
-                if (cls == 2) Aw[w][lane] = 1.f / Aw[w][lane];
+                const bool open = bmk == v;
+                const float aw = Aw[w][lane];
+                Aw[w][lane] = (cls == 2) ? (open ? 1.f / aw : 0.f) : (open ? aw : pinf());
             }
             const bool diag = (jb == ib);
             const bool upper = (qw0 - ib * G) >= 32;  // this wave holds queries 32-63 of its block
@@ -215,14 +216,12 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
                                                    : *reinterpret_cast<const f32x4 *>(&kSUFL[s4]);
                             if constexpr (CLS > 0) {
                                 const f32x4 bm4 = *reinterpret_cast<const f32x4 *>(&Bw[w][s4]);
-                                const f32x4 gt4 = *reinterpret_cast<const f32x4 *>(&Gw[w][s4]);
 #pragma unroll
                                 for (int e = 0; e < 4; ++e) {
                                     const int j = 4 * jq + e;
                                     const float P = fexp2(fmaf(S[j], p.sc2, bm4[e]));
                                     const float dS = P * dP[j];
-                                    const float gg = dS * gt4[e];
-                                    rblk = fmaf(gg, (CLS == 2) ? zk4[e] : frcp(zk4[e] + bq), rblk);
+                                    rblk = fmaf(dS, (CLS == 2) ? zk4[e] : frcp(zk4[e] + bq), rblk);
                                     S[j] = dS;
                                 }
                                 continue;
