@@ -103,12 +103,14 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
     float *sBM = dyn, *scanA = dyn + NB, *scanB = dyn + 2 * NB;
 
     // This lane's 16 gated in-block dS values (column s = lane, rows u in [16w, 16w + 16)),
-    // loaded first so that their latency overlaps the setup below.
+    // loaded first so that their latency overlaps the setup below.  A column with no row u > s in
+    // this range (s >= 16w + 15) has no pair here: its values are never read and are not loaded.
     f32x4 gq[4];
     {
         const f32x4 *gsrc = reinterpret_cast<const f32x4 *>(p.gd + ((brow + U) * G + lane) * G + 16 * w);
+        const bool need = lane < 16 * w + 15;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) gq[i] = gsrc[i];
+        for (int i = 0; i < 4; ++i) gq[i] = need ? gsrc[i] : f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
     if (U == 0 && b == 0) {  // dbeta[h] = sum over batches and key-side partials
