@@ -202,10 +202,17 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
             // the bias is cAz per key and the gate m_s <= psi_s is per key, so the block needs only
             // sum_t dS_ts per key (class 1).  When moreover 2^{BLSE - rs} <= 2^-25 for every key, each
             // Z_ts 2^{-rs} = sv + 2^{PREL_t - rs} equals sv to within 2^-25 (sv >= 1), below fp32
-            // resolution: the soft-min sum is sum_t g_ts / sv (class 2).
+            // resolution: the soft-min sum is sum_t g_ts / sv (class 2).  Otherwise, when the gate
+            // PRE_t <= thr is open for every row (PRE_t is non-increasing along the block, so it is
+            // enough that the block's first row passes for every key), g = dS (class 3, on the
+            // product form of Z only).
             int cls = 0;
-            if (FPA_KV_CLASSES && !diag && __all(bm_here >= fminf(suf, mid)))
-                cls = __all(bl_cur - rs <= -25.f) ? 2 : 1;
+            if (FPA_KV_CLASSES && !diag) {
+                if (__all(bm_here >= fminf(suf, mid)))
+                    cls = __all(bl_cur - rs <= -25.f) ? 2 : 1;
+                else if (prod && __all(rPRE[0] <= thr))
+                    cls = 3;
+            }
             float dsum = 0.f;  // classes 1, 2: sum of dS over the block
             // On the diagonal the upper 32 keys come after every one of the first 32 queries: that
             // quarter (all P = 0; its gd entries are never read) is skipped.
@@ -238,11 +245,11 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
 #pragma unroll
                             for (int e = 0; e < 4; ++e) {
                                 const int j = 4 * jq + e;
-                                if constexpr (CLS == 0) {
+                                if constexpr (CLS == 0 || CLS == 3) {
                                     const float bm = __builtin_amdgcn_fmed3f(fmaf(pre4[e], beff, nbpsi), cAz, E);
                                     const float P = fexp2(fmaf(S[j], p.sc2, bm));
                                     const float dS = P * dP[j];
-                                    const float gg = (pre4[e] <= thr) ? dS : 0.f;
+                                    const float gg = (CLS == 3 || pre4[e] <= thr) ? dS : 0.f;
                                     gsum += gg;
                                     dbacc = fmaf(dS, bm, dbacc);
                                     const float z = PROD ? fmaf(zq4[e], ck, sv) : sv + fexp2(zq4[e] - rsb);
@@ -268,6 +275,8 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
                     using C2 = std::integral_constant<int, 2>;
                     if (cls == 2)
                         offdiag(std::true_type{}, C2{});
+                    else if (cls == 3)
+                        offdiag(std::true_type{}, std::integral_constant<int, 3>{});
                     else if (cls == 1)
                         prod ? offdiag(std::true_type{}, C1{}) : offdiag(std::false_type{}, C1{});
                     else
@@ -305,7 +314,7 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
                     dkacc[dt] = mma_p2_p3_pad<T, DT, true>(dkacc[dt], dP, Qt, 32 * mt, 32 * (dt0 + dt), lane);
                 }
             }
-            if (cls > 0) {  // the per-key sums of classes 1 and 2
+            if (cls == 1 || cls == 2) {  // the per-key sums of classes 1 and 2
                 const bool gate = fminf(suf, mid) <= psi_s;
                 gsum += gate ? dsum : 0.f;
                 dbacc = fmaf(dsum, cAz, dbacc);

@@ -112,6 +112,8 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
         prel = p.state[L.at(PL_PREL, bh, tq)];
     }
     const float ct = -pre * p.il2;  // max a over [start of blk(t), t]
+    // PRE_t is non-increasing along a block: this is the largest PRE of the wave's queries.
+    const float premax = wave_max(t_valid ? pre : ninf());
     const float prel_ct = fexp2(prel - ct);
     const float E = (betal >= 0.f) ? ninf() : pinf();  // med3(x, y, E) = min (beta >= 0) or max (beta < 0)
 
@@ -183,6 +185,12 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
                 const bool open = bmk == v;
                 const float aw = Aw[w][lane];
                 Aw[w][lane] = (cls == 2) ? (open ? 1.f / aw : 0.f) : (open ? aw : pinf());
+            } else if (FPA_Q_CLASSES && fast) {
+                // Class 3: the gate x_ts <= 0 open for every pair.  x grows with PRE_t, so it is
+                // enough that it holds at the wave's largest PRE for every key of the block (lane =
+                // key); then bm = v and g = dS.
+                const float v = __builtin_amdgcn_fmed3f(kSUF[lane], betal * fminf(premax, mid), E) - kPSI[lane];
+                if (__all(__builtin_amdgcn_fmed3f(v, 0.f, E) == v)) cls = 3;
             }
             const bool diag = (jb == ib);
             const bool upper = (qw0 - ib * G) >= 32;  // this wave holds queries 32-63 of its block
@@ -214,7 +222,7 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
                             const int s4 = 32 * mt + 8 * jq + 4 * g;
                             const f32x4 zk4 = FAST ? *reinterpret_cast<const f32x4 *>(&Aw[w][s4])
                                                    : *reinterpret_cast<const f32x4 *>(&kSUFL[s4]);
-                            if constexpr (CLS > 0) {
+                            if constexpr (CLS == 1 || CLS == 2) {
                                 const f32x4 bm4 = *reinterpret_cast<const f32x4 *>(&Bw[w][s4]);
 #pragma unroll
                                 for (int e = 0; e < 4; ++e) {
@@ -234,10 +242,10 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
                                 // v = betal * x with x = min(SUF_s, MID, PRE_t) - psi_s, and the bias
                                 // bm = betal * min(x, 0); the gate x <= 0 is bm == v for either sign.
                                 const float v = __builtin_amdgcn_fmed3f(bsuf4[e], bY, E) - bpsi4[e];
-                                const float bm = __builtin_amdgcn_fmed3f(v, 0.f, E);
+                                const float bm = (CLS == 3) ? v : __builtin_amdgcn_fmed3f(v, 0.f, E);
                                 const float P = fexp2(fmaf(S[j], p.sc2, bm));
                                 const float dS = P * dP[j];
-                                const float gg = (bm == v) ? dS : 0.f;
+                                const float gg = (CLS == 3 || bm == v) ? dS : 0.f;
                                 if constexpr (FAST)
                                     rblk = fmaf(gg, frcp(zk4[e] + bq), rblk);
                                 else
@@ -250,6 +258,8 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
 #if FPA_Q_FAST
                     if (cls == 2)
                         offdiag(std::true_type{}, std::integral_constant<int, 2>{});
+                    else if (cls == 3)
+                        offdiag(std::true_type{}, std::integral_constant<int, 3>{});
                     else if (cls == 1)
                         offdiag(std::true_type{}, std::integral_constant<int, 1>{});
                     else if (fast)

@@ -551,6 +551,9 @@ __device__ __forceinline__ float wave_sum(float x) {
 __device__ __forceinline__ float wave_min(float x) {
     return wave_reduce(x, [](float a, float b) { return fminf(a, b); });
 }
+__device__ __forceinline__ float wave_max(float x) {
+    return wave_reduce(x, [](float a, float b) { return fmaxf(a, b); });
+}
 
 
 // State planes (float offsets): NPL per-position planes of TP floats per head, then two block planes.
