@@ -143,6 +143,17 @@ def test_negative_and_zero_beta(fpa):
     check(run_hip(fpa, q, k, v, phi, psi, beta, do), O.fpa_grads(q, k, v, phi, psi, beta, do), torch.float32)
 
 
+@pytest.mark.parametrize("drift", [0.0, 0.01])
+def test_signed_beta_many_blocks(fpa, drift):
+    """beta (-0.7, 0, 1.3) over 16 blocks in fp16: the per-key classes of both backward sides (per-key
+    bias, per-key soft-min denominators, open gate) are voted per block and must hold for either sign
+    of beta and for beta = 0."""
+    _say(f"[parity] beta = (-0.7, 0, 1.3), T=1000 D64 fp16, drift {drift}")
+    q, k, v, phi, psi, _, do = O.make_inputs(1, 3, 1000, 64, dtype=torch.float16, seed=33, drift=drift)
+    beta = torch.tensor([-0.7, 0.0, 1.3])
+    check(run_hip(fpa, q, k, v, phi, psi, beta, do), O.fpa_grads(q, k, v, phi, psi, beta, do), torch.float16)
+
+
 def test_scalar_beta_and_strided_views(fpa):
     """beta given as a Python float; q, k, v as permuted views of one (B, T, 3, H, D) tensor."""
     _say("[parity] scalar beta, permuted q/k/v views")
