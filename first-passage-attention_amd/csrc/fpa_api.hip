@@ -38,7 +38,7 @@ WsLayout ws_layout(int64_t B, int64_t H, int64_t T) {
     w.wsum = off;  off += align64(BH * TP);
     w.rsum = off;  off += align64(BH * TP);
     w.gd = off;    off += align64(BH * NB * G * G);
-    w.tbuf = off;  off += align64(BH * NB * NB * 2);
+    w.tbuf = off;  off += align64(BH * NB * NB);
     w.dbp = off;   off += align64(BH * NK32);
     w.total = off;
     return w;

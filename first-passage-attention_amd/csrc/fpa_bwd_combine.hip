@@ -89,6 +89,7 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
     __shared__ float segM[4][G], segZ[4][G], segM2[4][G], segZ2[4][G], segA[4][G], segB[4][G], pp[4][G];
     __shared__ float contrib[G][G + 1];      // [u][s]
     __shared__ float sF[G], sH[G];           // single-reference key-block and query-block terms
+    __shared__ float sE[G];                  // 2^{a_u - c_U} (0 past the block's last position)
     __shared__ float red[4];
 
     const int U = group_x(), bh = group_bh(p.H), b = bh / p.H, h = bh % p.H;
@@ -134,6 +135,14 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
         sc[tid] = (pre < pinf()) ? -pre * il2 : ninf();
         sW[tid] = p.wsum[r];
         sR[tid] = p.rsum[r];
+        {
+            // c_U = max a over the block = -BMIN * log2(e) / tau (the value sBM[U] holds below).  No
+            // FMA contraction here, so that the exponent is the one the LDS values give.
+#pragma clang fp contract(off)
+            const float cu = -p.state[L.bplane(BP_MIN) + brow + U] * il2;
+            const float au = (ph < pinf()) ? -ph * il2 : ninf();
+            sE[tid] = (tid <= last) ? fexp2(au - cu) : 0.f;
+        }
     }
     for (int i = tid; i < NB; i += NTHREADS) sBM[i] = -p.state[L.bplane(BP_MIN) + brow + i] * il2;
     __syncthreads();
@@ -152,8 +161,7 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
         for (int idx = tid; idx < npairs; idx += NTHREADS) {
             const int ib = U + 1 + idx / U, jb = idx % U;
             const float cm = fmaxf(fmaxf(scanA[jb + 1], cU), scanB[ib - 1]);
-            const float *tb = p.tbuf + ((brow + ib) * NB + jb) * 2;
-            acc += fexp2(cU - cm) * (tb[0] + tb[1]);
+            acc += fexp2(cU - cm) * p.tbuf[(brow + ib) * NB + jb];
         }
         SU = block_sum_256(acc, red, w, lane);
     }
@@ -177,7 +185,7 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
             const int u = u0 + k;
-            ev[k] = (u > s && u <= last) ? fexp2(sA[u] - cU) : 0.f;
+            ev[k] = (u > s) ? sE[u] : 0.f;  // sE is 0 past the last position
             Zs += ev[k];
         }
         segZ[w][s] = Zs;
@@ -297,7 +305,7 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
                     }
                     if (v >= u && v <= last) part += sH[v];
                 }
-                part *= fexp2(au - cU);
+                part *= sE[u];
             } else {
 #pragma unroll
                 for (int k = 0; k < 16; ++k) {

@@ -67,6 +67,7 @@ struct KvShared {
     __attribute__((aligned(1024))) char dOs[NS][TB];
     __attribute__((aligned(1024))) float qi[NS][QI_PLANES][64];  // per-query values of a block: LQ, DL, PRE, ZQ, BST
     __attribute__((aligned(16))) float kPHI[32 * NW];
+    float tpx[2][NW];  // each wave's middle-block sum of the last two query blocks (by parity)
 };
 
 // Keys [32 NW kt, 32 NW (kt + 1)) of head bh: every query block from the keys' diagonal block to T.
@@ -167,9 +168,19 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
     wait_loads();
     __syncthreads();
     constexpr int NS = KvShared<T, D, NW>::NS;
+    // TBUF holds one middle-block sum per (query block, key block) pair: the two waves of a 64-key
+    // block (2 h, 2 h + 1) add their halves through LDS once the barrier that ends the query block has
+    // passed, and the even wave writes the sum.
+    static_assert(NW % 2 == 0, "two waves per 64-key block");
+    auto flush_tbuf = [&](int ibp, int par) {
+        if ((w & 1) == 0 && lane == 0 && scalars && wave_active && ibp > jb + 1)
+            p.tbuf[(brow + ibp) * p.NB + jb] = sm.tpx[par][w] + sm.tpx[par][w + 1];
+    };
     for (int ib = ib0, it = 0; ib < p.NB; ++ib, ++it) {
         const int buf = (NS == 2) ? (it & 1) : 0;
         if constexpr (NS == 2) issue(umin_i(ib + 1, p.NB - 1), buf ^ 1);
+        if (it > 0) flush_tbuf(ib - 1, (it - 1) & 1);
+        float tpw = 0.f;
         const float bm_here = qi[buf][QI_BST][0], bl_cur = qi[buf][QI_BST][1];  // block ib
         if (wave_active && ib >= jb) {
             // Soft-min denominators off the diagonal: Z_ts 2^{-rs} = sv + 2^{PREL_t - rs} with the
@@ -322,12 +333,10 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
             }
             if (ib > jb) {  // close query block ib: key-block and middle-block soft-min sums
                 if (rs > ninf()) Wacc = fmaf(fexp2(Cs - rs), wblk, Wacc);
-                if (ib > jb + 1) {
-                    const float tp = wave_sum((rs > ninf()) ? fexp2(cmid - rs) * wblk : 0.f);
-                    if (lane == 0 && scalars) p.tbuf[((brow + ib) * p.NB + jb) * 2 + ((kw0 / 32) & 1)] = tp;
-                }
+                if (ib > jb + 1) tpw = wave_sum((rs > ninf()) ? fexp2(cmid - rs) * wblk : 0.f);
             }
         }
+        if (lane == 0) sm.tpx[it & 1][w] = tpw;
         if (wave_active && ib > jb) {  // block ib joins the middle of the blocks after it
             mid = fminf(mid, bm_here);
             midl = lse2_pair(midl, bl_cur);
@@ -343,6 +352,7 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
         __syncthreads();
     }
 
+    flush_tbuf(p.NB - 1, (p.NB - 1 - ib0) & 1);
     // Per-key outputs (lanes c and c + 32 hold the same key, different queries).
     gsum = sum_halves(gsum);
     Wacc = sum_halves(Wacc);

@@ -52,7 +52,7 @@ struct BwdParams {
     float *wsum;   // BH * TP   key-block soft-min sums W_s
     float *rsum;   // BH * TP   query-block soft-min sums R_t
     float *gd;     // BH * NB * G * G   gated dS of in-block pairs, [s][t]
-    float *tbuf;   // BH * NB * NB * 2  middle-block sums (two 32-key halves)
+    float *tbuf;   // BH * NB * NB      middle-block sums
     float *dbp;    // BH * NK32         dbeta partials, one per 32-key group
     int B, H, T, TP, NB, BH, NK32;
     float sc2;     // log2(e) / sqrt(D)
