@@ -12,8 +12,23 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_prep_kernel(BwdParams p) {
     constexpr int CPR = (D + CE - 1) / CE;
     const int bh = group_bh(p.H), b = bh / p.H, h = bh % p.H;
     const int row = group_x() * 64 + thread_x() / 4, part = thread_x() % 4;
+    const StateLayout L{p.BH, p.TP, p.NB};
+    const bool ok = row < p.T;
+    // The row's statistics first: their loads overlap those of O and dO below.
+    float blse = 0.f, prel0 = 0.f, prel = 0.f, pre = pinf(), bmin = 0.f, lse = 0.f;
+    const bool writer = part == 0 && row < p.TP;
+    if (writer) {
+        blse = p.state[L.bplane(BP_LSE) + (int64_t)bh * p.NB + row / G];
+        prel0 = p.state[L.at(PL_PREL, bh, (row / G) * G)];
+        if (ok) {
+            prel = p.state[L.at(PL_PREL, bh, row)];
+            pre = p.state[L.at(PL_PRE, bh, row)];
+            lse = p.lse[(int64_t)bh * p.TP + row];
+        }
+        if (row % G == 0) bmin = p.state[L.bplane(BP_MIN) + (int64_t)bh * p.NB + row / G];
+    }
     float acc = 0.f;
-    if (row < p.T) {
+    if (ok) {
         const T *Or = static_cast<const T *>(p.o) + b * p.so.b + h * p.so.h + (int64_t)row * p.so.t;
         const T *Dr = static_cast<const T *>(p.dout) + b * p.sdo.b + h * p.sdo.h + (int64_t)row * p.sdo.t;
         for (int cc = part; cc < CPR; cc += 4) {
@@ -32,20 +47,15 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_prep_kernel(BwdParams p) {
     }
     acc += __shfl_xor(acc, 1, 64);
     acc += __shfl_xor(acc, 2, 64);
-    if (part == 0 && row < p.TP) {
-        const StateLayout L{p.BH, p.TP, p.NB};
-        const int64_t r = (int64_t)bh * p.TP + row;
-        const bool ok = row < p.T;
-        const float blse = p.state[L.bplane(BP_LSE) + (int64_t)bh * p.NB + row / G];
-        const float prl = ok ? p.state[L.at(PL_PREL, bh, row)] - blse : 0.f;
-        const float spread = blse - p.state[L.at(PL_PREL, bh, (row / G) * G)];
-        const float beff = beta_eff(p.beta[bh % p.H] * LOG2E);
-        p.qinfo[qi_at(bh, p.NB, row, QI_LQ)] = ok ? -p.lse[r] / p.sc2 : ninf();
+    if (writer) {
+        const float prl = ok ? prel - blse : 0.f;
+        const float spread = blse - prel0;
+        p.qinfo[qi_at(bh, p.NB, row, QI_LQ)] = ok ? -lse / p.sc2 : ninf();
         p.qinfo[qi_at(bh, p.NB, row, QI_DL)] = ok ? -acc : 0.f;
-        p.qinfo[qi_at(bh, p.NB, row, QI_PRE)] = ok ? p.state[L.at(PL_PRE, bh, row)] : pinf();
+        p.qinfo[qi_at(bh, p.NB, row, QI_PRE)] = ok ? pre : pinf();
         p.qinfo[qi_at(bh, p.NB, row, QI_ZQ)] = (FPA_KV_PROD && spread <= PROD_SPREAD) ? fexp2(prl) : prl;
-        // The block's BMIN and BLSE for the key side's loop (plane 7, positions 0 and 1).
-        if (row % G < 2) p.qinfo[qi_at(bh, p.NB, row, QI_BST)] = (row % G == 0) ? p.state[L.bplane(BP_MIN) + (int64_t)bh * p.NB + row / G] : blse;
+        // The block's BMIN and BLSE for the key side's loop (plane QI_BST, positions 0 and 1).
+        if (row % G < 2) p.qinfo[qi_at(bh, p.NB, row, QI_BST)] = (row % G == 0) ? bmin : blse;
     }
 }
 
