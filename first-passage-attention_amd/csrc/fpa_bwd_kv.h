@@ -11,7 +11,7 @@
 //   dpsi_s  = -beta * sum_t g_ts                       (g = [x <= 0] dS, strict t > s)
 //   dbeta   = sum_{t>s} dS_ts min(0, x_ts)             (per-wave partials, summed later)
 //   W_s     = sum_{t outside blk(s)} g_ts 2^{C_s} / Z_ts   (key-block soft-min sums)
-//   TBUF    = middle-block soft-min sums per (query block, key block, key half)
+//   TBUF    = middle-block soft-min sums per (query block, key block)
 // and writes the in-block gated dS to GD for the in-block soft-min recurrence.
 #pragma once
 
