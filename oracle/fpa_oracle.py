@@ -115,6 +115,37 @@ def fpa_grads(q, k, v, phi, psi, beta, do, tau=1.0, dtype=torch.float64):
     return [o.detach()] + [g.detach() for g in grads]
 
 
+def fpa_grads_stored(q, k, v, phi, psi, beta, do, tau=1.0, store=torch.float16, dtype=torch.float64):
+    """fpa_grads with Delta_t = sum_d dO_td O~_td taken from O~, the forward output rounded to ``store``.
+
+    That is the Delta the reference's _bwd_delta (kernel.py:165-174) computes, from the output
+    tensor the forward stored in the input dtype (and so does the HIP prep kernel).  With it
+    dS_ts = P_ts (dP_ts - Delta~_t), the exact dS plus P_ts (Delta_t - Delta~_t); P_ts is the
+    derivative of the row's log-sum-exp lse_t by S_ts, so the gradients of
+    <o, dO> + sum_t (Delta_t - Delta~_t) lse_t, with the coefficients held fixed, are these.
+    o is returned exact.  With store = dtype the result is fpa_grads'.
+    """
+    H, T, D = q.shape[1], q.shape[2], q.shape[3]
+    b = beta if torch.is_tensor(beta) else torch.tensor(float(beta))
+    b = b.reshape(-1)
+    if b.numel() == 1:
+        b = b.expand(H)
+    args = [t.detach().cpu().to(dtype).requires_grad_() for t in (q, k, v, phi, psi)]
+    bb = b.detach().cpu().to(dtype).contiguous().requires_grad_()
+    qd, kd, vd, ph, ps = args
+    logits = torch.matmul(qd, kd.transpose(-1, -2)) / math.sqrt(D) + first_passage_bias(ph, ps, bb, tau)
+    causal = torch.ones(T, T, dtype=torch.bool).tril()
+    logits = logits.masked_fill(~causal, -math.inf)
+    lse = torch.logsumexp(logits, dim=-1)
+    o = torch.matmul(torch.exp(logits - lse.unsqueeze(-1)), vd)
+    dod = do.detach().cpu().to(dtype)
+    delta = (dod * o.detach()).sum(-1)
+    delta_stored = (dod * o.detach().to(store).to(dtype)).sum(-1)
+    loss = (o * dod).sum() + ((delta - delta_stored) * lse).sum()
+    grads = torch.autograd.grad(loss, args + [bb])
+    return [o.detach()] + [g.detach() for g in grads]
+
+
 def fpa_grads_chunked(q, k, v, phi, psi, beta, do, tau=1.0, dtype=torch.float64, device=None,
                       max_elems=1 << 27):
     """fpa_grads computed over chunks of query rows, for shapes whose (T, T) tensors are too big.

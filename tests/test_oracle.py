@@ -167,3 +167,33 @@ def test_chunked_oracle_is_the_dense_oracle(B, H, T, D, tau, scale, ties, drift,
         assert x.shape == r.shape, name
         assert O.rel_err(x, r) <= 1e-12, (name, O.rel_err(x, r))
 
+
+
+def test_stored_output_oracle():
+    """fpa_grads_stored: with no rounding it is fpa_grads; with the output stored in fp16 the gradients
+    move by exactly the closed-form change of dS, P_ts (Delta_t - Delta~_t), pushed through
+    dq = dS k / sqrt(D) and dk = dS^T q / sqrt(D); dv (P^T dO) does not move."""
+    B, H, T, D = 1, 2, 40, 16
+    q, k, v, phi, psi, beta, do = O.make_inputs(B, H, T, D, dtype=torch.float16, seed=77, phi_scale=2.0)
+    exact = O.fpa_grads(q, k, v, phi, psi, beta, do, tau=0.7)
+    same = O.fpa_grads_stored(q, k, v, phi, psi, beta, do, tau=0.7, store=torch.float64)
+    for x, y in zip(exact, same):
+        assert torch.allclose(x, y, rtol=1e-11, atol=1e-12)
+    st = O.fpa_grads_stored(q, k, v, phi, psi, beta, do, tau=0.7, store=torch.float16)
+    # Closed form of the change, from the float64 forward by the loop definition.
+    qd, kd, vd, dod = (t.double().numpy() for t in (q, k, v, do))
+    bias = O.bias_by_loops(phi.double().numpy(), psi.double().numpy(), beta.double().numpy())
+    for h in range(H):
+        z = qd[0, h] @ kd[0, h].T / np.sqrt(D) + bias[0, h]
+        z = np.where(np.tril(np.ones((T, T), bool)), z, -np.inf)
+        p = np.exp(z - z.max(-1, keepdims=True))
+        p /= p.sum(-1, keepdims=True)
+        o = p @ vd[0, h]
+        o16 = o.astype(np.float16).astype(np.float64)
+        change = p * ((dod[0, h] * o).sum(-1) - (dod[0, h] * o16).sum(-1))[:, None]
+        assert np.abs(change).max() > 0  # the rounding does change dS
+        dq_change = change @ kd[0, h] / np.sqrt(D)
+        dk_change = change.T @ qd[0, h] / np.sqrt(D)
+        assert np.allclose(st[1][0, h].numpy() - exact[1][0, h].numpy(), dq_change, rtol=1e-6, atol=1e-12)
+        assert np.allclose(st[2][0, h].numpy() - exact[2][0, h].numpy(), dk_change, rtol=1e-6, atol=1e-12)
+        assert np.allclose(st[3][0, h].numpy(), exact[3][0, h].numpy(), rtol=1e-11, atol=1e-12)
