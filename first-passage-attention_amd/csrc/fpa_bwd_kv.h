@@ -126,7 +126,9 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
     // exponent).  Off the diagonal, x = min(SUF_s, MID, PRE_t) - psi_s splits into a per-key part
     // and a per-query part: bm = beff * min(x, 0) = med3(beff PRE_t - beff psi_s, cAz, E) with
     // cAz = beff * min(SUF_s - psi_s, MID - psi_s, 0), and the gate x <= 0 is PRE_t <= thr with
-    // thr = +inf when min(SUF_s, MID) <= psi_s (every query passes), else psi_s.
+    // thr = +inf when min(SUF_s, MID) <= psi_s (every query passes), else psi_s.  With fp32
+    // operands x is formed before the scaling: x = min(PRE_t, mS) - psi_s with mS = min(SUF_s, MID,
+    // psi_s), bm = beff * x, cAz = beff * cx with cx = mS - psi_s, and dbeta sums dS x directly.
     const float beta = p.beta[h], beff = beta_eff(beta * LOG2E);
     const float E = (beff > 0.f) ? ninf() : pinf();  // med3(x, y, E) = min (beff > 0) or max
     float psi_s = 0.f, suf = pinf(), sufl = ninf();
@@ -137,6 +139,7 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
     }
     const float Cs = (suf < pinf()) ? -suf * p.il2 : ninf();  // max a over (s, end of block)
     const float bsuf = beff * suf, bpsi = beff * psi_s;
+    constexpr bool XB = exact_bias<T>();
     // Accumulator start values from a per-query plane of the staged block: register j of this
     // lane holds row 32 mt + 8 (j / 4) + 4 g + j % 4.
     auto rows16 = [&](const float *plane, int mt) {
@@ -197,7 +200,9 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
                 ck = fexp2(fminf(-rsb, 126.f));
                 prod = uniform_f(qi[buf][QI_ZQ][0]) > 0.f;
             }
-            const float cAz = __builtin_amdgcn_fmed3f(__builtin_amdgcn_fmed3f(bsuf, beff * mid, E) - bpsi, 0.f, E);
+            const float mS = fminf(fminf(suf, mid), psi_s), cx = mS - psi_s;
+            const float cAz = XB ? beff * cx
+                                 : __builtin_amdgcn_fmed3f(__builtin_amdgcn_fmed3f(bsuf, beff * mid, E) - bpsi, 0.f, E);
             const float thr = (fminf(suf, mid) <= psi_s) ? pinf() : psi_s;
             const float nbpsi = -bpsi;
             const char *Qt = Qs[buf];
@@ -257,12 +262,13 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
                             for (int e = 0; e < 4; ++e) {
                                 const int j = 4 * jq + e;
                                 if constexpr (CLS == 0 || CLS == 3) {
-                                    const float bm = __builtin_amdgcn_fmed3f(fmaf(pre4[e], beff, nbpsi), cAz, E);
+                                    const float xb = XB ? fminf(pre4[e], mS) - psi_s : 0.f;
+                                    const float bm = XB ? beff * xb : __builtin_amdgcn_fmed3f(fmaf(pre4[e], beff, nbpsi), cAz, E);
                                     const float P = fexp2(fmaf(S[j], p.sc2, bm));
                                     const float dS = P * dP[j];
                                     const float gg = (CLS == 3 || pre4[e] <= thr) ? dS : 0.f;
                                     gsum += gg;
-                                    dbacc = fmaf(dS, bm, dbacc);
+                                    dbacc = fmaf(dS, XB ? xb : bm, dbacc);
                                     const float z = PROD ? fmaf(zq4[e], ck, sv) : sv + fexp2(zq4[e] - rsb);
                                     wblk = fmaf(gg, frcp(z), wblk);
                                     S[j] = P;
@@ -310,7 +316,7 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
                             const float dS = P * dP[j];
                             const float gg = (x <= 0.f) ? dS : 0.f;
                             gsum += gg;
-                            dbacc = fmaf(dS, bm, dbacc);
+                            dbacc = fmaf(dS, XB ? fminf(x, 0.f) : bm, dbacc);
                             g4[e] = gg;
                             S[j] = P;
                             dP[j] = dS;
@@ -328,7 +334,7 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
             if (cls == 1 || cls == 2) {  // the per-key sums of classes 1 and 2
                 const bool gate = fminf(suf, mid) <= psi_s;
                 gsum += gate ? dsum : 0.f;
-                dbacc = fmaf(dsum, cAz, dbacc);
+                dbacc = fmaf(dsum, XB ? cx : cAz, dbacc);
                 wblk = !gate ? 0.f : (cls == 2) ? dsum / sv : wblk;
             }
             if (ib > jb) {  // close query block ib: key-block and middle-block soft-min sums
@@ -356,7 +362,7 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
     // Per-key outputs (lanes c and c + 32 hold the same key, different queries).
     gsum = sum_halves(gsum);
     Wacc = sum_halves(Wacc);
-    const float dbw = wave_sum(dbacc) / beff;
+    const float dbw = XB ? wave_sum(dbacc) : wave_sum(dbacc) / beff;
     if (!wave_active) return;
     if (scalars) {
         if (lane == 0) p.dbp[(int64_t)bh * p.NK32 + kw0 / 32] = dbw;  // one partial per 32-key group

@@ -45,7 +45,7 @@ struct QShared {
     static constexpr int NS = tile_stages<TB>(2 * 8 * 64 * 4 + NW * 64 * 4);
     __attribute__((aligned(1024))) char Ks[NS][TB];
     __attribute__((aligned(1024))) char Vs[NS][TB];
-    // Per-key values of a block: BSUF, CP (= betal * psi), SUFL, PHI, and BST (BMIN, BLSE, SUF of the
+    // Per-key values of a block: BSUF, CP (= betal * psi; SUF and PSI for fp32), SUFL, PHI, and BST (BMIN, BLSE, SUF of the
     // first key at [4][0..2]; planes 4-7 are four copies, so the two halves are one 1 KB load each
     // from the even and the odd waves).
     __attribute__((aligned(1024))) float kst[NS][8][64];
@@ -80,8 +80,10 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
     const T *Kb = static_cast<const T *>(p.k) + b * p.sk.b + h * p.sk.h;
     const T *Vb = static_cast<const T *>(p.v) + b * p.sv.b + h * p.sv.h;
     const T *DOb = static_cast<const T *>(p.dout) + b * p.sdo.b + h * p.sdo.h;
-    // lanes 0-15: BSUF, 16-31: CP, 32-47: SUFL, 48-63: PHI
-    const int kpl = (lane < 16) ? PL_BSUF : (lane < 32) ? PL_CP : (lane < 48) ? PL_SUFL : PL_PHI;
+    // lanes 0-15: BSUF, 16-31: CP, 32-47: SUFL, 48-63: PHI.  With fp32 operands SUF and PSI take the
+    // places of BSUF and CP: x = min(SUF_s, MID, PRE_t) - psi_s is formed before the scaling by betal.
+    constexpr bool XB = exact_bias<T>();
+    const int kpl = (lane < 16) ? (XB ? PL_SUF : PL_BSUF) : (lane < 32) ? (XB ? PL_PSI : PL_CP) : (lane < 48) ? PL_SUFL : PL_PHI;
     const float *st_head = p.state + L.at(0, bh, 0);
     const uint32_t kst_off = (uint32_t)((kpl * p.TP + 4 * (lane & 15)) * 4);  // bytes from plane 0 of the head
     const uint32_t bst_off = (uint32_t)((PL_BST * p.TP + 4 * (lane & 15)) * 4);  // four copies of BST
@@ -168,7 +170,7 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
                 }
             }
             float rblk = 0.f;  // sum of g / (Z 2^{-R}) over this key block (shared-reference path)
-            const float bY = betal * fminf(pre, mid);
+            const float bY = XB ? fminf(pre, mid) : betal * fminf(pre, mid);
             // Shared-reference path, when every query of the wave has PRE_t >= MID (the largest
             // min(SUF_s, MID) of a block is MID: its last key has an empty suffix), x_ts =
             // min(SUF_s, MID) - psi_s for all t: bias and gate are per key, tabled once per block
@@ -180,18 +182,31 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
             int cls = 0;
             if (FPA_Q_CLASSES && fast && __all(!t_valid || pre >= mid)) {
                 cls = __all(!t_valid || prel - midl <= -25.f) ? 2 : 1;
-                const float v = __builtin_amdgcn_fmed3f(kSUF[lane], betal * mid, E) - kPSI[lane];
-                const float bmk = __builtin_amdgcn_fmed3f(v, 0.f, E);
-                Bw[w][lane] = bmk;
-                const bool open = bmk == v;
+                bool open;
+                if constexpr (XB) {
+                    const float x = fminf(kSUF[lane], mid) - kPSI[lane];
+                    Bw[w][lane] = betal * fminf(x, 0.f);
+                    open = x <= 0.f;
+                } else {
+                    const float v = __builtin_amdgcn_fmed3f(kSUF[lane], betal * mid, E) - kPSI[lane];
+                    const float bmk = __builtin_amdgcn_fmed3f(v, 0.f, E);
+                    Bw[w][lane] = bmk;
+                    open = bmk == v;
+                }
                 const float aw = Aw[w][lane];
                 Aw[w][lane] = (cls == 2) ? (open ? 1.f / aw : 0.f) : (open ? aw : pinf());
             } else if (FPA_Q_CLASSES && fast) {
                 // Class 3: the gate x_ts <= 0 open for every pair.  x grows with PRE_t, so it is
                 // enough that it holds at the wave's largest PRE for every key of the block (lane =
                 // key); then bm = v and g = dS.
-                const float v = __builtin_amdgcn_fmed3f(kSUF[lane], betal * fminf(premax, mid), E) - kPSI[lane];
-                if (__all(__builtin_amdgcn_fmed3f(v, 0.f, E) == v)) cls = 3;
+                bool open;
+                if constexpr (XB) {
+                    open = fminf(kSUF[lane], fminf(premax, mid)) <= kPSI[lane];
+                } else {
+                    const float v = __builtin_amdgcn_fmed3f(kSUF[lane], betal * fminf(premax, mid), E) - kPSI[lane];
+                    open = __builtin_amdgcn_fmed3f(v, 0.f, E) == v;
+                }
+                if (__all(open)) cls = 3;
             }
             const bool diag = (jb == ib);
             const bool upper = (qw0 - ib * G) >= 32;  // this wave holds queries 32-63 of its block
@@ -242,11 +257,20 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
                                 const int j = 4 * jq + e;
                                 // v = betal * x with x = min(SUF_s, MID, PRE_t) - psi_s, and the bias
                                 // bm = betal * min(x, 0); the gate x <= 0 is bm == v for either sign.
-                                const float v = __builtin_amdgcn_fmed3f(bsuf4[e], bY, E) - bpsi4[e];
-                                const float bm = (CLS == 3) ? v : __builtin_amdgcn_fmed3f(v, 0.f, E);
+                                float bm;
+                                bool open;
+                                if constexpr (XB) {  // bsuf4, bpsi4 hold SUF and psi, bY min(PRE_t, MID)
+                                    const float x = fminf(bsuf4[e], bY) - bpsi4[e];
+                                    bm = betal * ((CLS == 3) ? x : fminf(x, 0.f));
+                                    open = x <= 0.f;
+                                } else {
+                                    const float v = __builtin_amdgcn_fmed3f(bsuf4[e], bY, E) - bpsi4[e];
+                                    bm = (CLS == 3) ? v : __builtin_amdgcn_fmed3f(v, 0.f, E);
+                                    open = bm == v;
+                                }
                                 const float P = fexp2(fmaf(S[j], p.sc2, bm));
                                 const float dS = P * dP[j];
-                                const float gg = (CLS == 3 || bm == v) ? dS : 0.f;
+                                const float gg = (CLS == 3 || open) ? dS : 0.f;
                                 if constexpr (FAST)
                                     rblk = fmaf(gg, frcp(zk4[e] + bq), rblk);
                                 else
@@ -279,7 +303,9 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
                             const int s = s0 + s4 + e;
                             const bool valid = t_valid && (s <= tq);
                             const bool strict = valid && (s < tq);
-                            const float bm = strict ? __builtin_amdgcn_fmed3f(fmaf(betal, X[j], -bpsi4[e]), 0.f, E) : 0.f;
+                            const float bm = !strict ? 0.f
+                                             : XB ? betal * fminf(X[j] - bpsi4[e], 0.f)
+                                                  : __builtin_amdgcn_fmed3f(fmaf(betal, X[j], -bpsi4[e]), 0.f, E);
                             const float P = valid ? fexp2(fmaf(S[j], p.sc2, bm)) : 0.f;
                             S[j] = P * dP[j];
                         }

@@ -571,6 +571,16 @@ struct StateLayout {
 // PL_BST holds, at positions 0, 1, 2 of each block, the block's BMIN, BLSE and SUF of its first
 // position (0 elsewhere): staged with a tile, the kernels read them from LDS, never from memory
 // inside their loops.
+// How the kernels form the bias beta * min(0, x), x = m - psi_s (m a minimum of PRE, SUF and MID
+// values).  For fp32 operands they subtract first and scale after: x is exact when m and psi_s are
+// close, as the float32 evaluation of the formula is.  Scaling first, betal * m - betal * psi_s,
+// rounds betal * psi_s on its own: phi is a walk whose values reach hundreds at long T, and at
+// |betal * psi_s| = 300 that rounding moves every bias of key s by up to 1.5e-5 (base 2), an
+// error per key that the sums of dS over queries in dbeta do not cancel.  The fp16 path scales
+// first (one VALU operation less per element): its error there is far below what fp16 resolves.
+template <typename T>
+constexpr bool exact_bias() { return sizeof(T) == 4; }
+
 enum { PL_PHI = 0, PL_PSI = 1, PL_PRE = 2, PL_PREL = 3, PL_SUF = 4, PL_SUFL = 5, PL_CA = 6, PL_CP = 7, PL_BSUF = 8,
        PL_BST = 9 };
 enum { BP_MIN = 0, BP_LSE = 1 };

@@ -104,7 +104,9 @@ hipError_t launch_stats(const StatsParams &p, hipStream_t s) {
 // staged in LDS and one per-query value in a register:
 //   b2 = med3(A_s, Y_t - P_s, E),  A_s = beta*log2e*min(SUF_s - psi_s, 0),
 //   P_s = beta*log2e*psi_s, Y_t = beta*log2e*min(PRE_t, MID), E = -inf (beta >= 0) or +inf,
-// which is beta*log2e*min(0, min(SUF_s, MID, PRE_t) - psi_s) for either sign of beta.
+// which is beta*log2e*min(0, min(SUF_s, MID, PRE_t) - psi_s) for either sign of beta.  With fp32
+// operands the staged values are SUF_s and psi_s instead, Y_t = min(PRE_t, MID), and the bias is
+// beta*log2e*(min(Y_t, SUF_s, psi_s) - psi_s): the subtraction comes before the scaling.
 // On the diagonal block X_ts = min phi(s, t] comes from a scan down the block.
 // The running max is only moved when a row's tile max exceeds it by more than 8 (base 2):
 // p <= 256 and the O rescale is skipped on most tiles.
@@ -121,7 +123,7 @@ fpa_fwd_kernel(FwdParams p) {
     constexpr int NS = tile_stages<TB>(2 * 4 * BN * 4);
     __shared__ __attribute__((aligned(1024))) char Ks[NS][TB];
     __shared__ __attribute__((aligned(1024))) char Vs[NS][TB];
-    // Per-key values of a tile: CA, CP, PHI and BST (the block's BMIN at [3][0]).
+    // Per-key values of a tile: CA, CP (SUF, PSI for fp32), PHI and BST (the block's BMIN at [3][0]).
     __shared__ __attribute__((aligned(1024))) float cst[NS][4][BN];
 
     const int tid = thread_x(), lane = tid % 64, g = lane / 32, c = lane % 32;
@@ -143,7 +145,9 @@ fpa_fwd_kernel(FwdParams p) {
     // Per-key values staged with one 64-lane load: lanes 0-15 CA, 16-31 CP, 32-47 PHI, 48-63 BST (byte
     // offsets from plane 0 of the head; the state planes hold TP >= every tile end rows).
     const float *st_head = p.state + L.at(0, bh, 0);
-    const uint32_t cst_off = (uint32_t)((((lane < 16) ? PL_CA : (lane < 32) ? PL_CP : (lane < 48) ? PL_PHI : PL_BST) * p.TP + 4 * (lane & 15)) * 4);
+    constexpr bool XB = exact_bias<T>();
+    const int cpl = (lane < 16) ? (XB ? PL_SUF : PL_CA) : (lane < 32) ? (XB ? PL_PSI : PL_CP) : (lane < 48) ? PL_PHI : PL_BST;
+    const uint32_t cst_off = (uint32_t)((cpl * p.TP + 4 * (lane & 15)) * 4);
 
     // Tile jt of K, V and the per-key values into buffer `buf` (shared out over the waves; every wave
     // issues the per-key load, identical writes instead of a wave-dependent branch).  After tile 0
@@ -186,7 +190,7 @@ fpa_fwd_kernel(FwdParams p) {
             const float *cA = cst[buf][0], *cP = cst[buf][1], *cPHI = cst[buf][2];
             const int jb = jt;  // BN == G: the key tile is one statistics block
             const bool diag = (jb == ib);
-            const float Y = betal * fminf(pre_t, mid);
+            const float Y = XB ? fminf(pre_t, mid) : betal * fminf(pre_t, mid);
             const int tr = tq - s0;
             float r = pinf();  // running min of phi over [u, t] for the in-block scan
             // Both 32-key halves' scores first; then each half in turn (the second half's MFMAs
@@ -205,7 +209,8 @@ fpa_fwd_kernel(FwdParams p) {
                         const f32x4 p4 = *reinterpret_cast<const f32x4 *>(&cP[s4]);
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
-                            const float b2 = __builtin_amdgcn_fmed3f(a4[e], Y - p4[e], E);
+                            const float b2 = XB ? betal * (fminf(fminf(Y, a4[e]), p4[e]) - p4[e])
+                                                : __builtin_amdgcn_fmed3f(a4[e], Y - p4[e], E);
                             s[mt][4 * jq + e] = fmaf(s[mt][4 * jq + e], p.sc2, b2);
                         }
                     }
@@ -220,7 +225,8 @@ fpa_fwd_kernel(FwdParams p) {
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const int j = 4 * jq + e, sr = s4 + e;
-                            const float bx = __builtin_amdgcn_fmed3f(0.f, fmaf(betal, X[j], -p4[e]), E);
+                            const float bx = XB ? betal * fminf(X[j] - p4[e], 0.f)
+                                                : __builtin_amdgcn_fmed3f(0.f, fmaf(betal, X[j], -p4[e]), E);
                             const float b2 = (sr < tr) ? bx : 0.f;  // b_tt = 0
                             const float z = fmaf(s[mt][j], p.sc2, b2);
                             s[mt][j] = (sr > tr || s0 + sr >= p.T) ? ninf() : z;

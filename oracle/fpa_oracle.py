@@ -115,7 +115,8 @@ def fpa_grads(q, k, v, phi, psi, beta, do, tau=1.0, dtype=torch.float64):
     return [o.detach()] + [g.detach() for g in grads]
 
 
-def fpa_grads_stored(q, k, v, phi, psi, beta, do, tau=1.0, store=torch.float16, dtype=torch.float64):
+def fpa_grads_stored(q, k, v, phi, psi, beta, do, tau=1.0, store=torch.float16, dtype=torch.float64,
+                     o_stored=None):
     """fpa_grads with Delta_t = sum_d dO_td O~_td taken from O~, the forward output rounded to ``store``.
 
     That is the Delta the reference's _bwd_delta (kernel.py:165-174) computes, from the output
@@ -123,7 +124,8 @@ def fpa_grads_stored(q, k, v, phi, psi, beta, do, tau=1.0, store=torch.float16, 
     dS_ts = P_ts (dP_ts - Delta~_t), the exact dS plus P_ts (Delta_t - Delta~_t); P_ts is the
     derivative of the row's log-sum-exp lse_t by S_ts, so the gradients of
     <o, dO> + sum_t (Delta_t - Delta~_t) lse_t, with the coefficients held fixed, are these.
-    o is returned exact.  With store = dtype the result is fpa_grads'.
+    o is returned exact.  With store = dtype the result is fpa_grads'.  ``o_stored``, when given, is
+    the stored output itself (the forward's result, with its own rounding) and replaces O~.
     """
     H, T, D = q.shape[1], q.shape[2], q.shape[3]
     b = beta if torch.is_tensor(beta) else torch.tensor(float(beta))
@@ -140,7 +142,8 @@ def fpa_grads_stored(q, k, v, phi, psi, beta, do, tau=1.0, store=torch.float16, 
     o = torch.matmul(torch.exp(logits - lse.unsqueeze(-1)), vd)
     dod = do.detach().cpu().to(dtype)
     delta = (dod * o.detach()).sum(-1)
-    delta_stored = (dod * o.detach().to(store).to(dtype)).sum(-1)
+    os_ = o.detach().to(store) if o_stored is None else o_stored.detach().cpu()
+    delta_stored = (dod * os_.to(dtype)).sum(-1)
     loss = (o * dod).sum() + ((delta - delta_stored) * lse).sum()
     grads = torch.autograd.grad(loss, args + [bb])
     return [o.detach()] + [g.detach() for g in grads]

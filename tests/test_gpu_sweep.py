@@ -8,21 +8,21 @@ and soft-min classes, open gates, product or exact soft-min forms) around.  The 
 reference's (test.py:18-20): max |x - ref| / max |ref| <= 2e-3 in fp16 (1e-2 for dbeta) and 2e-4
 in fp32.
 
-The draws stay in the reference's data model (psi = phi + noise of at most 0.5, phi scale up to 4):
-dbeta is sum_ts dS_ts b_ts / beta, and every row of dS sums to zero, so its relative error grows
-with sum |dS b| / |dbeta|.  With psi noise 2, phi scale 8 and tau 0.5 that ratio reaches 2.5e4 and a
-float32 evaluation misses the bound as well (6e-3 against 2e-4), so such inputs test conditioning
-rather than the kernels.
+The backward's Delta_t = sum_d dO_td O_td reads the output as the forward stored it, as the
+reference's _bwd_delta does (kernel.py:165-174): in fp16 that output is rounded to fp16, in fp32
+it carries the forward's own rounding.  dbeta and dphi sum dS_ts over many pairs whose rows
+cancel (every row of dS sums to zero), so that difference alone moves them by up to several
+percent on some draws.  The gradients are therefore checked against ``fpa_grads_stored`` given
+the kernel's own output (the float64 gradients with Delta from that output, everything else
+exact), and o against the exact forward.
 
-In fp16 the backward's Delta_t = sum_d dO_td O_td reads the output as stored, in fp16, as the
-reference's _bwd_delta does (kernel.py:165-174); that rounding alone moves dphi by up to 3e-3 of
-its largest value on some draws (it is not a kernel error: against a float64 reference that takes
-the same rounded output, the kernels agree to 4e-5 there).  So fp16 gradients are checked against
-``fpa_grads_stored``, the float64 gradients with Delta from the output rounded to fp16; o against
-the exact forward.  dbeta sums dS_ts b_ts, whose rows cancel, so on some draws it moves by several
-percent when the stored output is rounded (the exact and the stored references differ by that
-much); an fp16 output one unit off in a few places moves it as far again, so fp16 dbeta is held
-to the larger of the usual bound and twice that measured sensitivity.
+The draws stay in the reference's data model (psi = phi + noise of at most 0.5, phi scale up to 4).
+The long draws (16 to 32 blocks) keep to beta > 0, the reference's domain (kernel.py:7).  With
+beta < 0 the bias is positive and grows with the range of the walk: at T = 1531 and phi scale 4
+the logits and lse reach 630 (base 2), where an fp32 exponent is good to 3e-5, and any evaluation
+that recomputes P from a stored fp32 lse (the reference's backward, kernel.py:216, as well as
+this one) moves dbeta, whose condition number sum |dS x| / |dbeta| is 2.5e4 there, by about 1e-2.
+Negative and mixed beta are drawn at the shorter lengths, where the bias stays small.
 """
 import random
 import sys
@@ -31,30 +31,33 @@ import pytest
 import torch
 
 from oracle import fpa_oracle as O
-from test_gpu_parity import NAMES, TOL, TOL_DBETA_FP16, check, run_hip
+from test_gpu_parity import check, run_hip
 
 pytestmark = pytest.mark.gpu
 
 
-def _cases(n=16, seed=2026):
+def _cases(n=16, seed=2026, lengths=(1, 37, 64, 129, 200, 333, 512, 701), first=1000,
+           betas=("positive", "negative", "mixed", "zero")):
     rng = random.Random(seed)
     out = []
     for i in range(n):
         out.append(dict(
             B=rng.choice([1, 2]), H=rng.choice([1, 2, 3]),
-            T=rng.choice([1, 37, 64, 129, 200, 333, 512, 701]),
+            T=rng.choice(lengths),
             D=rng.choice([16, 32, 64, 128]),
             dtype=rng.choice(["f16", "f32"]),
-            beta=rng.choice(["positive", "negative", "mixed", "zero"]),
+            beta=rng.choice(betas),
             tau=rng.choice([0.5, 1.0, 2.0]),
             phi_scale=rng.choice([0.3, 1.0, 4.0]),
             drift=rng.choice([0.0, 0.02]),
             psi_noise=rng.choice([0.1, 0.25, 0.5]),
-            seed=1000 + i))
+            seed=first + i))
     return out
 
 
-CASES = _cases()
+# Short and ragged lengths, then six draws over 16 to 32 blocks (more off-diagonal blocks per tile,
+# so every per-block class occurs), beta > 0.
+CASES = _cases() + _cases(n=6, seed=7, lengths=(1000, 1531, 2048), first=2000, betas=("positive",))
 
 
 def _say(*a):
@@ -91,15 +94,6 @@ def test_sweep_matches_the_oracle(fpa, case):
         beta = torch.zeros(c["H"])
     kern = run_hip(fpa, q, k, v, phi, psi, beta, do, tau=c["tau"])
     exact = O.fpa_grads(q, k, v, phi, psi, beta, do, tau=c["tau"])
-    if dtype == torch.float32:
-        check(kern, exact, dtype)
-        return
-    ref = O.fpa_grads_stored(q, k, v, phi, psi, beta, do, tau=c["tau"], store=torch.float16)
-    check(kern[:6], ref[:6], dtype)
-    db, db_ref, db_exact = kern[6], ref[6], exact[6]
-    assert db.dtype == torch.float32 and torch.isfinite(db).all()
-    scale = db_ref.abs().max().item()
-    sens = (db_ref - db_exact).abs().max().item() / scale
-    err = O.rel_err(db, db_ref)
-    _say(f"  dbeta err {err:.2e}, sensitivity to the stored output {sens:.2e}")
-    assert err <= max(TOL_DBETA_FP16, 2 * sens), ("dbeta", err, sens)
+    check(kern[:1], exact[:1], dtype)
+    ref = O.fpa_grads_stored(q, k, v, phi, psi, beta, do, tau=c["tau"], o_stored=kern[0])
+    check(kern, [exact[0]] + ref[1:], dtype)

@@ -197,3 +197,21 @@ def test_stored_output_oracle():
         assert np.allclose(st[1][0, h].numpy() - exact[1][0, h].numpy(), dq_change, rtol=1e-6, atol=1e-12)
         assert np.allclose(st[2][0, h].numpy() - exact[2][0, h].numpy(), dk_change, rtol=1e-6, atol=1e-12)
         assert np.allclose(st[3][0, h].numpy(), exact[3][0, h].numpy(), rtol=1e-11, atol=1e-12)
+    # o_stored: the stored output given directly.  The exact output rounded to fp16 gives the same
+    # gradients as store=float16; any other output moves dS by P_ts (Delta_t - Delta~_t) with
+    # Delta~ from it, through dq as above.
+    given = O.fpa_grads_stored(q, k, v, phi, psi, beta, do, tau=0.7, o_stored=exact[0].to(torch.float16))
+    for x, y in zip(st, given):
+        assert torch.equal(x, y)
+    g = torch.Generator().manual_seed(5)
+    o_other = exact[0] + 1e-3 * torch.randn(exact[0].shape, generator=g, dtype=torch.float64)
+    other = O.fpa_grads_stored(q, k, v, phi, psi, beta, do, tau=0.7, store=torch.float64, o_stored=o_other)
+    for h in range(H):
+        z = qd[0, h] @ kd[0, h].T / np.sqrt(D) + bias[0, h]
+        z = np.where(np.tril(np.ones((T, T), bool)), z, -np.inf)
+        p = np.exp(z - z.max(-1, keepdims=True))
+        p /= p.sum(-1, keepdims=True)
+        change = p * ((dod[0, h] * (p @ vd[0, h])).sum(-1) - (dod[0, h] * o_other[0, h].numpy()).sum(-1))[:, None]
+        assert np.allclose(other[1][0, h].numpy() - exact[1][0, h].numpy(), change @ kd[0, h] / np.sqrt(D),
+                           rtol=1e-6, atol=1e-12)
+        assert np.allclose(other[3][0, h].numpy(), exact[3][0, h].numpy(), rtol=1e-11, atol=1e-12)
