@@ -510,8 +510,10 @@ inline dim3 head_grid(int n, int H, int BH) { return dim3(n, H, BH / H); }
 // Work item of this workgroup in a per-head grid of ntiles workgroups per head: rank 0 is the
 // heaviest tile.  Workgroups are dispatched in linear order (x fastest, then the head), round-
 // robin over the 8 XCDs of the chip; when BH is a multiple of 8 every head is pinned to one XCD
-// (its K/V stay in that XCD's L2) and each XCD takes its heads' tiles heaviest first.  The
-// entry points keep ntiles * BH below 2^31.
+// (its K/V stay in that XCD's L2) and each XCD takes its heads' tiles heaviest first.  Otherwise
+// the dispatch order is rank-major over all heads (every head's heaviest tile first), so that the
+// longest tiles never wait for a free slot behind the short tiles of earlier heads.  The entry
+// points keep ntiles * BH below 2^31.
 __device__ __forceinline__ void xcd_work_item(int &rank, int &bh, int BH, int H, int ntiles) {
     const int L = group_x() + ntiles * group_bh(H);
     if ((BH & 7) == 0) {
@@ -519,8 +521,8 @@ __device__ __forceinline__ void xcd_work_item(int &rank, int &bh, int BH, int H,
         rank = k / hpx;
         bh = (k % hpx) * 8 + xcd;
     } else {
-        rank = group_x();
-        bh = group_bh(H);
+        rank = L / BH;
+        bh = L % BH;
     }
     rank = __builtin_amdgcn_readfirstlane(rank);  // uniform: loop bounds and addresses stay scalar
     bh = __builtin_amdgcn_readfirstlane(bh);
