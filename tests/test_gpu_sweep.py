@@ -2,7 +2,7 @@
 
 The fixed cases (test_gpu_parity.py) follow the reference's test matrix (test.py:134-147); this
 sweep draws further combinations from one seeded generator: ragged lengths, every head
-dimension up to 128, both dtypes, beta of either sign or zero per head, tau, the phi scale and
+dimension up to 256, both dtypes, beta of either sign or zero per head, tau, the phi scale and
 drift, and the psi noise, which together move the backward's per-block decisions (per-key bias
 and soft-min classes, open gates, product or exact soft-min forms) around.  The bounds are the
 reference's (test.py:18-20): max |x - ref| / max |ref| <= 2e-3 in fp16 (1e-2 for dbeta) and 2e-4
@@ -37,14 +37,14 @@ pytestmark = pytest.mark.gpu
 
 
 def _cases(n=16, seed=2026, lengths=(1, 37, 64, 129, 200, 333, 512, 701), first=1000,
-           betas=("positive", "negative", "mixed", "zero")):
+           betas=("positive", "negative", "mixed", "zero"), dims=(16, 32, 64, 128)):
     rng = random.Random(seed)
     out = []
     for i in range(n):
         out.append(dict(
             B=rng.choice([1, 2]), H=rng.choice([1, 2, 3]),
             T=rng.choice(lengths),
-            D=rng.choice([16, 32, 64, 128]),
+            D=rng.choice(dims),
             dtype=rng.choice(["f16", "f32"]),
             beta=rng.choice(betas),
             tau=rng.choice([0.5, 1.0, 2.0]),
@@ -55,9 +55,10 @@ def _cases(n=16, seed=2026, lengths=(1, 37, 64, 129, 200, 333, 512, 701), first=
     return out
 
 
-# Short and ragged lengths, then six draws over 16 to 32 blocks (more off-diagonal blocks per tile,
-# so every per-block class occurs), beta > 0.
-CASES = _cases() + _cases(n=6, seed=7, lengths=(1000, 1531, 2048), first=2000, betas=("positive",))
+# Short and ragged lengths; six draws over 16 to 32 blocks (more off-diagonal blocks per tile, so
+# every per-block class occurs), beta > 0; six draws at D = 256 (the single-wave-per-SIMD kernels).
+CASES = (_cases() + _cases(n=6, seed=7, lengths=(1000, 1531, 2048), first=2000, betas=("positive",))
+         + _cases(n=6, seed=11, lengths=(3, 65, 190, 449, 640), first=3000, dims=(256,)))
 
 
 def _say(*a):
