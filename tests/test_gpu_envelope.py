@@ -78,14 +78,16 @@ def _row_reference(q, k, v, phi, psi, beta, t):
     return p @ vd[: t + 1]
 
 
-def test_length_beyond_131072(fpa):
-    """T = 131269 (2052 blocks of 64, past the earlier 2048-block cap), one head, fp16 D16.
+@pytest.mark.parametrize("T", [131269, 524288])
+def test_length_beyond_131072(fpa, T):
+    """T = 131269 (2052 blocks of 64, past the earlier 2048-block cap) and T = 524288 (8192 blocks,
+    the largest the library takes), one head, fp16 D16.
 
     With dO zero on every row >= T0 = 320, each output and gradient of positions < T0 equals that
     of the T0-long problem on the same prefix (which is itself checked against the oracle) and
     every gradient of positions >= T0 is zero.  The far rows of o are checked against a float64
     restatement of the definition, one row at a time."""
-    T, T0, D = 131269, 320, 16
+    T0, D = 320, 16
     _say(f"[envelope] T={T} (NB={(T + 63) // 64}), prefix T0={T0}, D={D} fp16")
     q, k, v, phi, psi, beta, do = O.make_inputs(1, 1, T, D, dtype=torch.float16, seed=420, beta="ones")
     do[:, :, T0:] = 0
@@ -104,7 +106,7 @@ def test_length_beyond_131072(fpa):
         if name != "o":
             assert (xb[:, :, T0:] == 0).all(), name
     o = big[0][0, 0]
-    for t in (T - 1, T - 1000, 131072):
+    for t in (T - 1, T - 1000, T // 2 + 17, 131072):
         ref = _row_reference(q[0, 0], k[0, 0], v[0, 0], phi[0, 0], psi[0, 0], 1.0, t)
         err = (o[t].double() - ref).abs().max().item() / ref.abs().max().item()
         assert err <= 2e-3, (t, err)
