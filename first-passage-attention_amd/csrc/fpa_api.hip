@@ -126,7 +126,7 @@ int64_t fpa_state_floats(int64_t B, int64_t H, int64_t T) {
     return StateLayout{B * H, TP, TP / G}.total();
 }
 
-int64_t fpa_lse_floats(int64_t B, int64_t H, int64_t T) { return B * H * tp_of(T); }
+int64_t fpa_lse_floats(int64_t B, int64_t H, int64_t T) { return 2 * B * H * tp_of(T); }
 
 int64_t fpa_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D, int32_t dtype) {
     (void)D;

@@ -230,13 +230,16 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
                     cls = 3;
             }
             float dsum = 0.f;  // classes 1, 2: sum of dS over the block
+            // fp32: the block's dbeta terms dS x are summed on their own and added to dbacc once per
+            // block (the terms cancel: every row of dS sums to zero, and |x| reaches hundreds).
+            float dbblk = 0.f;
             // On the diagonal the upper 32 keys come after every one of the first 32 queries: that
             // quarter (all P = 0; its gd entries are never read) is skipped.
 #pragma unroll 1
             for (int mt = (diag && upper) ? 1 : 0; mt < 2; ++mt) {
                 f32x16 S, dP;
                 // S - lse / sc2 and dP - Delta, rows t, columns s
-                S = rows16(qi[buf][QI_LQ], mt);
+                S = XB ? zero16() : rows16(qi[buf][QI_LQ], mt);
                 dP = rows16(qi[buf][QI_DL], mt);
                 mma_p1_pad_reg2<T, D, DT>(S, Qt, 32 * mt + c, kreg, dP, Dt, 32 * mt + c, vreg, g);
                 float X[16];
@@ -257,6 +260,11 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
                         for (int jq = 0; jq < 4; ++jq) {
                             const int t4 = 32 * mt + 8 * jq + 4 * g;
                             const f32x4 pre4 = *reinterpret_cast<const f32x4 *>(&rPRE[t4]);
+                            f32x4 m4, l4;  // fp32: the rows' running maxima and log2 l
+                            if constexpr (XB) {
+                                m4 = *reinterpret_cast<const f32x4 *>(&qi[buf][QI_LQ][t4]);
+                                l4 = *reinterpret_cast<const f32x4 *>(&qi[buf][QI_LL][t4]);
+                            }
                             const f32x4 zq4 = *reinterpret_cast<const f32x4 *>(&rZQ[t4]);
 #pragma unroll
                             for (int e = 0; e < 4; ++e) {
@@ -264,17 +272,20 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
                                 if constexpr (CLS == 0 || CLS == 3) {
                                     const float xb = XB ? fminf(pre4[e], mS) - psi_s : 0.f;
                                     const float bm = XB ? beff * xb : __builtin_amdgcn_fmed3f(fmaf(pre4[e], beff, nbpsi), cAz, E);
-                                    const float P = fexp2(fmaf(S[j], p.sc2, bm));
+                                    const float P = fexp2(XB ? (fmaf(S[j], p.sc2, bm) - m4[e]) - l4[e] : fmaf(S[j], p.sc2, bm));
                                     const float dS = P * dP[j];
                                     const float gg = (CLS == 3 || pre4[e] <= thr) ? dS : 0.f;
                                     gsum += gg;
-                                    dbacc = fmaf(dS, XB ? xb : bm, dbacc);
+                                    if constexpr (XB)
+                                        dbblk = fmaf(dS, xb, dbblk);
+                                    else
+                                        dbacc = fmaf(dS, bm, dbacc);
                                     const float z = PROD ? fmaf(zq4[e], ck, sv) : sv + fexp2(zq4[e] - rsb);
                                     wblk = fmaf(gg, frcp(z), wblk);
                                     S[j] = P;
                                     dP[j] = dS;
                                 } else {
-                                    const float P = fexp2(fmaf(S[j], p.sc2, cAz));
+                                    const float P = fexp2(XB ? (fmaf(S[j], p.sc2, cAz) - m4[e]) - l4[e] : fmaf(S[j], p.sc2, cAz));
                                     const float dS = P * dP[j];
                                     dsum += dS;
                                     if constexpr (CLS == 1) {
@@ -302,7 +313,11 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
 #pragma unroll
                     for (int jq = 0; jq < 4; ++jq) {
                         const int t4 = 32 * mt + 8 * jq + 4 * g;
-                        f32x4 g4;
+                        f32x4 g4, m4, l4;
+                        if constexpr (XB) {
+                            m4 = *reinterpret_cast<const f32x4 *>(&qi[buf][QI_LQ][t4]);
+                            l4 = *reinterpret_cast<const f32x4 *>(&qi[buf][QI_LL][t4]);
+                        }
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const int j = 4 * jq + e;
@@ -312,11 +327,15 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
                             const bool valid = (t >= s) && s_valid;  // rows past T have -inf scores: P = 0
                             const float x = X[j] - psi_s;
                             const float bm = beff * fminf(x, 0.f);
-                            const float P = valid ? fexp2(fmaf(S[j], p.sc2, bm)) : 0.f;
+                            const float P = !valid ? 0.f
+                                            : fexp2(XB ? (fmaf(S[j], p.sc2, bm) - m4[e]) - l4[e] : fmaf(S[j], p.sc2, bm));
                             const float dS = P * dP[j];
                             const float gg = (x <= 0.f) ? dS : 0.f;
                             gsum += gg;
-                            dbacc = fmaf(dS, XB ? fminf(x, 0.f) : bm, dbacc);
+                            if constexpr (XB)
+                                dbblk = fmaf(dS, fminf(x, 0.f), dbblk);
+                            else
+                                dbacc = fmaf(dS, bm, dbacc);
                             g4[e] = gg;
                             S[j] = P;
                             dP[j] = dS;
@@ -331,6 +350,7 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
                     dkacc[dt] = mma_p2_p3_pad<T, DT, true>(dkacc[dt], dP, Qt, 32 * mt, 32 * (dt0 + dt), lane);
                 }
             }
+            if constexpr (XB) dbacc += dbblk;
             if (cls == 1 || cls == 2) {  // the per-key sums of classes 1 and 2
                 const bool gate = fminf(suf, mid) <= psi_s;
                 gsum += gate ? dsum : 0.f;

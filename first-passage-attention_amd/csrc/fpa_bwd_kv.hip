@@ -15,7 +15,8 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_prep_kernel(BwdParams p) {
     const StateLayout L{p.BH, p.TP, p.NB};
     const bool ok = row < p.T;
     // The row's statistics first: their loads overlap those of O and dO below.
-    float blse = 0.f, prel0 = 0.f, prel = 0.f, pre = pinf(), bmin = 0.f, lse = 0.f;
+    constexpr bool XB = exact_bias<T>();
+    float blse = 0.f, prel0 = 0.f, prel = 0.f, pre = pinf(), bmin = 0.f, lse = 0.f, lsl = 0.f;
     const bool writer = part == 0 && row < p.TP;
     if (writer) {
         blse = p.state[L.bplane(BP_LSE) + (int64_t)bh * p.NB + row / G];
@@ -24,6 +25,7 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_prep_kernel(BwdParams p) {
             prel = p.state[L.at(PL_PREL, bh, row)];
             pre = p.state[L.at(PL_PRE, bh, row)];
             lse = p.lse[(int64_t)bh * p.TP + row];
+            if constexpr (XB) lsl = p.lse[((int64_t)p.BH + bh) * p.TP + row];
         }
         if (row % G == 0) bmin = p.state[L.bplane(BP_MIN) + (int64_t)bh * p.NB + row / G];
     }
@@ -50,7 +52,12 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_prep_kernel(BwdParams p) {
     if (writer) {
         const float prl = ok ? prel - blse : 0.f;
         const float spread = blse - prel0;
-        p.qinfo[qi_at(bh, p.NB, row, QI_LQ)] = ok ? -lse / p.sc2 : ninf();
+        if constexpr (XB) {  // the row's running maximum (+inf past T: P = 0) and log2 l
+            p.qinfo[qi_at(bh, p.NB, row, QI_LQ)] = ok ? lse : pinf();
+            p.qinfo[qi_at(bh, p.NB, row, QI_LL)] = ok ? lsl : 0.f;
+        } else {
+            p.qinfo[qi_at(bh, p.NB, row, QI_LQ)] = ok ? -lse / p.sc2 : ninf();
+        }
         p.qinfo[qi_at(bh, p.NB, row, QI_DL)] = ok ? -acc : 0.f;
         p.qinfo[qi_at(bh, p.NB, row, QI_PRE)] = ok ? pre : pinf();
         p.qinfo[qi_at(bh, p.NB, row, QI_ZQ)] = (FPA_KV_PROD && spread <= PROD_SPREAD) ? fexp2(prl) : prl;

@@ -107,9 +107,10 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
     load_row_p1<T, D>(doreg, DOb + (int64_t)tq * p.sdo.t, t_valid, g);
 
     const float betal = p.beta[h] * LOG2E;
-    float lse = pinf(), del = 0.f, pre = 0.f, prel = 0.f;
+    float lse = pinf(), lsl = 0.f, del = 0.f, pre = 0.f, prel = 0.f;
     if (t_valid) {
-        lse = p.lse[rowbase + tq];
+        lse = p.lse[rowbase + tq];  // fp32: the row's running maximum
+        if constexpr (XB) lsl = p.lse[(int64_t)p.BH * p.TP + rowbase + tq];
         del = -p.qinfo[qi_at(bh, p.NB, tq, QI_DL)];
         pre = p.state[L.at(PL_PRE, bh, tq)];
         prel = p.state[L.at(PL_PREL, bh, tq)];
@@ -122,11 +123,13 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
 
     // The S and dP accumulators start at -lse_t / sc2 and -Delta_t (this lane's query, the same in
     // all 16 registers): the MFMA chains subtract them for free.  Rows past T get lse = +inf, so
-    // their scores are -inf and P = 0 with no per-element mask.
+    // their scores are -inf and P = 0 with no per-element mask.  fp32: S starts at 0, and the
+    // logit is formed as in the forward and shifted by the forward's running maximum and log2 l,
+    // P = 2^{(s - m) - log2 l}, so that P is the forward's to a few ulps whatever the size of s.
     f32x16 lq16, dl16;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-        lq16[j] = -lse / p.sc2;
+        lq16[j] = XB ? 0.f : -lse / p.sc2;
         dl16[j] = -del;
     }
 
@@ -243,7 +246,7 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
 #pragma unroll
                                 for (int e = 0; e < 4; ++e) {
                                     const int j = 4 * jq + e;
-                                    const float P = fexp2(fmaf(S[j], p.sc2, bm4[e]));
+                                    const float P = fexp2(XB ? (fmaf(S[j], p.sc2, bm4[e]) - lse) - lsl : fmaf(S[j], p.sc2, bm4[e]));
                                     const float dS = P * dP[j];
                                     rblk = fmaf(dS, (CLS == 2) ? zk4[e] : frcp(zk4[e] + bq), rblk);
                                     S[j] = dS;
@@ -268,7 +271,7 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
                                     bm = (CLS == 3) ? v : __builtin_amdgcn_fmed3f(v, 0.f, E);
                                     open = bm == v;
                                 }
-                                const float P = fexp2(fmaf(S[j], p.sc2, bm));
+                                const float P = fexp2(XB ? (fmaf(S[j], p.sc2, bm) - lse) - lsl : fmaf(S[j], p.sc2, bm));
                                 const float dS = P * dP[j];
                                 const float gg = (CLS == 3 || open) ? dS : 0.f;
                                 if constexpr (FAST)
@@ -306,7 +309,8 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
                             const float bm = !strict ? 0.f
                                              : XB ? betal * fminf(X[j] - bpsi4[e], 0.f)
                                                   : __builtin_amdgcn_fmed3f(fmaf(betal, X[j], -bpsi4[e]), 0.f, E);
-                            const float P = valid ? fexp2(fmaf(S[j], p.sc2, bm)) : 0.f;
+                            const float P = !valid ? 0.f
+                                            : fexp2(XB ? (fmaf(S[j], p.sc2, bm) - lse) - lsl : fmaf(S[j], p.sc2, bm));
                             S[j] = P * dP[j];
                         }
                     }

@@ -317,7 +317,14 @@ fpa_fwd_kernel(FwdParams p) {
                 }
             }
     }
-    if (g == 0 && tq < p.TP) p.lse[rowbase + tq] = m_i + flog2(l_i);
+    if (g == 0 && tq < p.TP) {
+        if constexpr (XB) {  // fp32: the running maximum and log2 l, for the backward's P = 2^{(s - m) - log2 l}
+            p.lse[rowbase + tq] = m_i;
+            p.lse[(int64_t)p.BH * p.TP + rowbase + tq] = flog2(l_i);
+        } else {
+            p.lse[rowbase + tq] = m_i + flog2(l_i);
+        }
+    }
 }
 
 template <typename T, int D>

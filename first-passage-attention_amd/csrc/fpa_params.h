@@ -76,8 +76,9 @@ struct FieldParams {
 
 // BwdParams::qinfo holds, per 64-query block of a head, QI_PLANES planes of 64 floats
 // ([bh][block][plane][64]), so the key side stages a block's first four planes with one 1 KB load.
-// QI_BST holds the block's BMIN and BLSE at positions 0 and 1; planes 5-7 are unused.
-enum { QI_LQ = 0, QI_DL = 1, QI_PRE = 2, QI_ZQ = 3, QI_BST = 4, QI_PLANES = 8 };
+// QI_BST holds the block's BMIN and BLSE at positions 0 and 1; QI_LL (fp32 only) each row's log2 l;
+// planes 6-7 are unused.
+enum { QI_LQ = 0, QI_DL = 1, QI_PRE = 2, QI_ZQ = 3, QI_BST = 4, QI_LL = 5, QI_PLANES = 8 };
 __host__ __device__ inline int64_t qi_at(int64_t bh, int NB, int row, int plane) {
     return ((bh * NB + row / 64) * QI_PLANES + plane) * 64 + row % 64;
 }

@@ -58,8 +58,10 @@ extern "C" {
  * phi/psi, addressed with element strides s*[0..3] = (b, h, t, d); the d stride
  * must be 1.  phi, psi, beta are float32; beta is (H,) contiguous.  lse and
  * state are contiguous float32 buffers the forward fills and the backward reads:
- * lse holds B*H*TP floats (TP = T rounded up to 64; base-2 log-sum-exp of each
- * query row), state holds fpa_state_floats(B, H, T) floats (block statistics).  */
+ * lse holds 2*B*H*TP floats (TP = T rounded up to 64): for fp16 the base-2
+ * log-sum-exp of each query row in the first B*H*TP; for fp32 the row's running
+ * maximum there and log2 of its sum in the second half.  state holds
+ * fpa_state_floats(B, H, T) floats (block statistics).  */
 typedef struct {
     int64_t B, H, T, D;
     int32_t dtype;
@@ -147,7 +149,7 @@ int fpa_field_bwd(const FpaFieldBwdArgs *args, void *stream);
 /* Floats of the forward state (block statistics) for a (B, H, T) problem. */
 int64_t fpa_state_floats(int64_t B, int64_t H, int64_t T);
 
-/* Floats of lse for a (B, H, T) problem (B * H * TP). */
+/* Floats of lse for a (B, H, T) problem (2 * B * H * TP). */
 int64_t fpa_lse_floats(int64_t B, int64_t H, int64_t T);
 
 /* Bytes of backward scratch for a (B, H, T, D) problem. */

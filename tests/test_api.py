@@ -64,7 +64,7 @@ def test_size_queries():
     L = _lib.lib()
     B, H, T = 2, 3, 100
     TP, NB = 128, 2
-    assert L.fpa_lse_floats(B, H, T) == B * H * TP
+    assert L.fpa_lse_floats(B, H, T) == 2 * B * H * TP
     assert L.fpa_state_floats(B, H, T) == 10 * B * H * TP + 2 * B * H * NB
     ws = L.fpa_bwd_workspace_bytes(B, H, T, 64, 0)
     assert ws % 256 == 0 and ws >= 4 * (3 * B * H * TP + B * H * NB * 64 * 64)
