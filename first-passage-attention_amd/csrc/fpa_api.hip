@@ -115,7 +115,7 @@ int hip_fail(hipError_t e, const char *where) {
 
 extern "C" {
 
-int fpa_abi_version(void) { return 3; }
+int fpa_abi_version(void) { return 4; }
 
 const char *fpa_source_hash(void) { return FPA_SOURCE_HASH; }
 

@@ -11,7 +11,7 @@ import torch
 
 from ._srchash import source_hash
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libfpa.so")
 
 FPA_F16, FPA_F32 = 0, 1

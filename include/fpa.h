@@ -174,7 +174,7 @@ int fpa_bwd_noalloc(const FpaBwdArgs *args, void *stream);
 /* Message of the last failed call on this host thread ("" if none). */
 const char *fpa_last_error(void);
 
-/* ABI version (bumped whenever the structs above change). */
+/* ABI version (bumped whenever the structs above or the buffer sizes change). */
 int fpa_abi_version(void);
 
 /* Hash of the sources the library was built from (16 hex digits; "unknown" when the build did
