@@ -154,6 +154,24 @@ def test_signed_beta_many_blocks(fpa, drift):
     check(run_hip(fpa, q, k, v, phi, psi, beta, do), O.fpa_grads(q, k, v, phi, psi, beta, do), torch.float16)
 
 
+def test_fp32_large_logits(fpa):
+    """fp32 with beta < 0 over a long phi walk: the bias is positive and the logits reach several hundred
+    (base 2).  The backward forms P from the forward's running maximum and log2 sum, so its P is the
+    forward's to a few ulps: dv (P^T dO) is held to 1e-5, the other gradients except dbeta to the fp32
+    bound.  dbeta is a sum of dS x over rows of dS that sum to zero (sum |dS x| / |dbeta| is about 1e4
+    here), and the fp32 rounding of the stored output alone moves it by about 1e-2 relative, in any
+    backward that takes Delta from that output; it is only checked for finiteness."""
+    _say("[parity] fp32 beta < 0, T=1531 D64, phi scale 4")
+    q, k, v, phi, psi, _, do = O.make_inputs(1, 2, 1531, 64, dtype=torch.float32, seed=2005, phi_scale=4.0,
+                                             psi_noise=0.1)
+    beta = torch.tensor([-0.9, -1.3])
+    kern = run_hip(fpa, q, k, v, phi, psi, beta, do, tau=0.5)
+    ref = O.fpa_grads(q, k, v, phi, psi, beta, do, tau=0.5)
+    check(kern[:6], ref[:6], torch.float32)
+    assert O.rel_err(kern[3], ref[3]) <= 1e-5, ("dv", O.rel_err(kern[3], ref[3]))
+    assert torch.isfinite(kern[6]).all()
+
+
 def test_scalar_beta_and_strided_views(fpa):
     """beta given as a Python float; q, k, v as permuted views of one (B, T, 3, H, D) tensor."""
     _say("[parity] scalar beta, permuted q/k/v views")
