@@ -39,7 +39,7 @@ pytestmark = pytest.mark.gpu
 
 def _cases(n=16, seed=2026, lengths=(1, 37, 64, 129, 200, 333, 512, 701), first=1000,
            betas=("positive", "negative", "mixed", "zero"), dims=(16, 32, 64, 128), ties=False,
-           dtypes=("f16", "f32")):
+           dtypes=("f16", "f32"), taus=(0.5, 1.0, 2.0)):
     rng = random.Random(seed)
     out = []
     for i in range(n):
@@ -49,7 +49,7 @@ def _cases(n=16, seed=2026, lengths=(1, 37, 64, 129, 200, 333, 512, 701), first=
             D=rng.choice(dims),
             dtype=rng.choice(dtypes),
             beta=rng.choice(betas),
-            tau=rng.choice([0.5, 1.0, 2.0]),
+            tau=rng.choice(taus),
             phi_scale=rng.choice([0.3, 1.0, 4.0]),
             drift=rng.choice([0.0, 0.02]),
             psi_noise=rng.choice([0.1, 0.25, 0.5]),
@@ -61,11 +61,13 @@ def _cases(n=16, seed=2026, lengths=(1, 37, 64, 129, 200, 333, 512, 701), first=
 # Short and ragged lengths; six draws over 16 to 32 blocks (more off-diagonal blocks per tile, so
 # every per-block class occurs), beta > 0; six draws at D = 256 (the single-wave-per-SIMD kernels); six
 # with phi rounded to integers (equal values inside ranges: tied minima and equal soft-min weights); four
-# long fp16 draws with beta of either sign.
+# long fp16 draws with beta of either sign; six at extreme temperatures (tau 0.1: the soft-min weights
+# near one-hot over spans of a few units of phi; tau 8: near-uniform).
 CASES = (_cases() + _cases(n=6, seed=7, lengths=(1000, 1531, 2048), first=2000, betas=("positive",))
          + _cases(n=6, seed=11, lengths=(3, 65, 190, 449, 640), first=3000, dims=(256,))
          + _cases(n=6, seed=13, lengths=(97, 256, 511, 800), first=4000, ties=True)
-         + _cases(n=4, seed=17, lengths=(1000, 1531, 2048), first=5000, betas=("negative", "mixed"), dtypes=("f16",)))
+         + _cases(n=4, seed=17, lengths=(1000, 1531, 2048), first=5000, betas=("negative", "mixed"), dtypes=("f16",))
+         + _cases(n=6, seed=19, lengths=(64, 300, 777), first=6000, betas=("positive", "mixed"), taus=(0.1, 8.0)))
 
 
 def _say(*a):
