@@ -46,17 +46,19 @@ WsLayout ws_layout(int64_t B, int64_t H, int64_t T) {
 
 S3 s3(const int64_t *s) { return S3{s[0], s[1], s[2]}; }
 
-// Field scratch: the projection (or its gradient) as B * 3H * T floats, then the dW / dbias partials.
+// Field scratch: the projection (or its gradient) as B * 3H rows of TL = T rounded up to 16 floats,
+// then the dW / dbias partials.
 struct FieldLayout {
     int64_t lin, part, total;  // float offsets
     int S;
 };
+int64_t field_tl(int64_t T) { return (T + 15) / 16 * 16; }
 FieldLayout field_layout(int64_t B, int64_t T, int64_t C, int64_t H) {
     FieldLayout f;
     const int64_t N = B * T;
     f.S = (int)((N + 255) / 256 < 64 ? (N + 255) / 256 : 64);
     f.lin = 0;
-    f.part = align64(B * 3 * H * T + 96);  // the dW kernel reads up to 96 floats past a position
+    f.part = align64(B * 3 * H * field_tl(T));
     f.total = f.part + align64((int64_t)f.S * 3 * H * (C + 1));  // the bias is feature C
     return f;
 }
@@ -66,7 +68,7 @@ int check_field(int64_t B, int64_t T, int64_t C, int64_t H, int32_t dtype, const
     if (B < 1 || T < 1 || C < 1 || H < 1) return fail(FPA_ERR_INVALID, "x must be (B, T, C) with B, T, C >= 1 and n_heads >= 1");
     if (dtype != FPA_F16 && dtype != FPA_F32) return fail(FPA_ERR_INVALID, "x must be fp16 or fp32");
     if (H > 32) return fail(FPA_ERR_UNSUPPORTED, "the Field kernels take at most 32 heads");
-    if (B > 65535 || B * T >= (int64_t(1) << 31) || C > (int64_t(1) << 24))
+    if (B > 65535 || B * field_tl(T) >= (int64_t(1) << 31) || C > (int64_t(1) << 24))
         return fail(FPA_ERR_UNSUPPORTED, "x is too large for the Field kernels");
     if (!x || !weight || !ws) return fail(FPA_ERR_INVALID, "x, weight and workspace must be non-NULL");
     if (sx[0] < 0 || sx[1] < 0) return fail(FPA_ERR_INVALID, "x strides must be non-negative");
@@ -151,6 +153,7 @@ int fpa_field_fwd(const FpaFieldFwdArgs *a, void *stream) {
     p.lin = static_cast<float *>(a->workspace) + fl.lin;
     p.phi = a->phi; p.psi = a->psi;
     p.B = (int)a->B; p.T = (int)a->T; p.C = (int)a->C; p.H = (int)a->H; p.NO = 3 * (int)a->H; p.S = fl.S;
+    p.TL = (int)field_tl(a->T);
     const hipError_t e = launch_field_fwd(p, a->dtype, reinterpret_cast<hipStream_t>(stream));
     return e != hipSuccess ? hip_fail(e, "fpa_field_fwd launch") : FPA_OK;
 }
@@ -173,6 +176,7 @@ int fpa_field_bwd(const FpaFieldBwdArgs *a, void *stream) {
     p.dphi = a->dphi; p.dpsi = a->dpsi;
     p.dw = a->dweight; p.dbias = a->dbias;
     p.B = (int)a->B; p.T = (int)a->T; p.C = (int)a->C; p.H = (int)a->H; p.NO = 3 * (int)a->H; p.S = fl.S;
+    p.TL = (int)field_tl(a->T);
     const hipError_t e = launch_field_bwd(p, a->dtype, reinterpret_cast<hipStream_t>(stream));
     return e != hipSuccess ? hip_fail(e, "fpa_field_bwd launch") : FPA_OK;
 }

@@ -6,13 +6,15 @@
 // and the gradient torch's autograd takes through it (kernel.py relies on autograd).
 //
 // The projection has only 3H outputs per position (36 for H = 12), so it is a pass over x
-// (HBM-bound) rather than a GEMM for the matrix cores.  A lane owns one position and the waves
-// of a workgroup split the features; the weights, the same for every lane, are scalar loads
-// used as SGPR operands, so no LDS traffic feeds the FMAs.  The projection is written per
-// (batch, output) along t, so the cumulative sum over t reads contiguous rows.  Backward: a
-// reverse cumulative sum gives d(delta); dx = d(lin) W is the same pass the other way round;
-// dW = d(lin)^T x (and dbias, as a feature of ones) is summed in a fixed order (per-split
-// partials, then one ordered reduction), so reruns are bit-identical.
+// (HBM-bound) with little arithmetic, done on the fp32 MFMA (the reference computes it in fp32).
+// With x aligned to four features (the usual case) the 16x16x4 kernels load x, W and d(lin) as
+// 16-byte vectors straight into MFMA operands, using the freedom to order the contraction so that
+// one four-feature load feeds four MFMAs; other layouts take the 32x32x2 kernels, which read one
+// element per lane.  The projection is stored per (batch, output) along t, in rows of TL = T
+// rounded up to 16, so the cumulative sum over t reads contiguous rows.  Backward: a reverse
+// cumulative sum gives d(delta) (the gradient is stored in the same layout, zero past T); dx =
+// d(lin) W is the same pass the other way round; dW = d(lin)^T x (and dbias) is summed in a fixed
+// order (per-split partials, then one ordered reduction), so reruns are bit-identical.
 #include <type_traits>
 
 #include "fpa_common.h"
@@ -27,8 +29,9 @@ constexpr int FT = 64;  // positions per workgroup (one per lane)
 template <typename TX> __device__ __forceinline__ float to_f(TX v) { return (float)v; }
 __device__ __forceinline__ int imin(int a, int b) { return a < b ? a : b; }  // per lane
 
-// Inclusive scan of one value per thread over a 256-thread workgroup (fixed order).
-__device__ __forceinline__ float block_scan256(float v, float *red) {
+// Inclusive scan of one value per thread over a 256-thread workgroup (fixed order); total gets the
+// sum of all 256 values.
+__device__ __forceinline__ float block_scan256(float v, float *red, float &total) {
     const int tid = thread_x(), lane = tid % 64, w = tid / 64;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -39,6 +42,7 @@ __device__ __forceinline__ float block_scan256(float v, float *red) {
     __syncthreads();
     float off = 0.f;
     for (int i = 0; i < w; ++i) off += red[i];
+    total = ((red[0] + red[1]) + red[2]) + red[3];
     __syncthreads();
     return v + off;
 }
@@ -139,55 +143,197 @@ __global__ void __launch_bounds__(64 * NWF) fpa_field_proj_kernel(FieldParams p)
         float v = 0.f;
 #pragma unroll
         for (int k = 0; k < NWF; ++k) v += lds[(k * NOP + o) * RP + lane];
-        p.lin[((int64_t)b * p.NO + o) * p.T + t] = v + p.bias[o];
+        p.lin[((int64_t)b * p.NO + o) * p.TL + t] = v + p.bias[o];
     }
 }
 
-// phi = cumsum_t(delta) + g, psi = cumsum_t(delta) + h for one (b, h) per workgroup (256 threads,
-// each a contiguous run of positions).
+// fp32 16x16x4 MFMA, A[m][k] x B[k][n] per wave: lane l gives A[l % 16][l / 16] and B[l / 16][l % 16];
+// register r of the 16x16 accumulator holds row 4 (l / 16) + r, column l % 16.
+__device__ __forceinline__ f32x4 mma16_f32(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Four consecutive features of x as one load (16 bytes in fp32, 8 in fp16), widened to fp32.
+template <typename TX> __device__ __forceinline__ f32x4 load4(const TX *a);
+template <> __device__ __forceinline__ f32x4 load4<float>(const float *a) { return *reinterpret_cast<const f32x4 *>(a); }
+template <> __device__ __forceinline__ f32x4 load4<f16>(const f16 *a) {
+    return __builtin_convertvector(*reinterpret_cast<const h4 *>(a), f32x4);
+}
+
+// lin on the 16x16x4 MFMA, x loaded straight into A operands: needs C, x's strides and the x and W
+// pointers aligned to four features.  Grid (ceil(T / (16 MT)), B), NWF waves; wave w owns features
+// [w CS, (w + 1) CS) for the workgroup's 16 MT positions (MT M tiles) and 16 NT >= NO outputs (N
+// tiles).  Per
+// 16-feature step, lane (k group j = l / 16, row r = l % 16) loads features c + 4j .. c + 4j + 3 of
+// each of its MT positions and of each of its W rows, and k step s of the four contracts feature
+// c + 4j + s: one 4-feature load feeds four MFMAs, x is read once, and no LDS is involved.  Loads
+// run PD steps ahead in a ring of registers; nothing is done to the loaded values before their
+// MFMAs (rows past T or NO read an in-bounds row, and only give sums that are never stored), so
+// the waits for a step's loads fall just before its products.  A last step of 4, 8 or 12 features
+// (C not a multiple of 16) zeroes the W values past the wave's features.  The NWF partial sums of
+// a position meet in LDS and are added in wave order.
+template <typename TX, int NT, int NWF, int PD, int MT, int LG>
+__global__ void __launch_bounds__(64 * NWF) fpa_field_proj16_kernel(FieldParams p) {
+    static_assert(PD % LG == 0, "loads are issued LG steps at a time");
+    constexpr int NOP = 16 * NT, FM = 16 * MT, RP = FM + 1;
+    __shared__ float red[NWF * NOP * RP];
+    const int tid = thread_x(), lane = tid % 64, j = lane / 16, r16 = lane % 16;
+    const int w = __builtin_amdgcn_readfirstlane(tid / 64);
+    const int b = group_y(), t0 = group_x() * FM;
+    const int CS = ((p.C + NWF - 1) / NWF + 15) / 16 * 16;
+    const int ca = umin_i(w * CS, p.C), cb = umin_i(ca + CS, p.C);
+    const TX *xb = static_cast<const TX *>(p.x) + (int64_t)b * p.sxb;
+    const TX *xrow[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const int t = t0 + 16 * mt + r16;
+        xrow[mt] = xb + (int64_t)(t < p.T ? t : p.T - 1) * p.sxt + 4 * j;
+    }
+    const float *wrow[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const int o = 16 * nt + r16;
+        wrow[nt] = p.w + (int64_t)(o < p.NO ? o : 0) * p.C + 4 * j;
+    }
+    const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+    f32x4 xr[PD][MT], wr[PD][NT], acc[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = z4;
+    auto load = [&](f32x4 (&xv)[MT], f32x4 (&wv)[NT], int c) {  // features c + 4j .. c + 4j + 3 (< C)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) xv[mt] = load4<TX>(xrow[mt] + c);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) wv[nt] = *reinterpret_cast<const f32x4 *>(wrow[nt] + c);
+        __builtin_amdgcn_sched_barrier(0);  // steps' loads stay in step order
+    };
+    auto step = [&](const f32x4 (&xv)[MT], const f32x4 (&wv)[NT]) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = mma16_f32(xv[mt][ks], wv[nt][ks], acc[mt][nt]);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    const int nfull = (cb - ca) / 16;  // whole 16-feature steps
+    if (nfull > 0) {
+        // Loads are issued unconditionally, so the waits count them exactly; those past the last whole
+        // step repeat its addresses (cache hits) and are not used.
+        const int clast = ca + 16 * (nfull - 1);
+#pragma unroll
+        for (int u = 0; u < PD; ++u) load(xr[u], wr[u], umin_i(ca + 16 * u, clast));
+        for (int s0 = 0; s0 < nfull; s0 += PD) {
+#pragma unroll
+            for (int h = 0; h < PD; h += LG) {
+#pragma unroll
+                for (int u = h; u < h + LG; ++u)
+                    if (s0 + u < nfull) step(xr[u], wr[u]);
+#pragma unroll
+                for (int u = h; u < h + LG; ++u) load(xr[u], wr[u], umin_i(ca + 16 * (s0 + u + PD), clast));
+            }
+        }
+    }
+    if (ca + 16 * nfull < cb) {  // the last 4, 8 or 12 features of x
+        const int c = ca + 16 * nfull;
+        load(xr[0], wr[0], c + 4 * j < cb ? c : c - 4 * j);  // lanes past cb read features c .. c + 3
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) wr[0][nt] = c + 4 * j < cb ? wr[0][nt] : z4;
+        step(xr[0], wr[0]);
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[(w * NOP + 16 * nt + r16) * RP + 16 * mt + 4 * j + r] = acc[mt][nt][r];
+    __syncthreads();
+    for (int i = tid; i < p.NO * FM; i += 64 * NWF) {
+        const int o = i / FM, r = i % FM, t = t0 + r;
+        if (t >= p.T) continue;
+        float v = 0.f;
+#pragma unroll
+        for (int k = 0; k < NWF; ++k) v += red[(k * NOP + o) * RP + r];
+        p.lin[((int64_t)b * p.NO + o) * p.TL + t] = v + p.bias[o];
+    }
+}
+
+constexpr int SCK = 8;  // 256-position chunks whose loads a scan issues together
+
+// phi = cumsum_t(delta) + g, psi = cumsum_t(delta) + h for one (b, h) per workgroup (256 threads):
+// 256 consecutive positions at a time, one per thread (coalesced rows), scanned across the
+// workgroup and added to the running total of the positions before them; the loads of SCK chunks
+// are issued before their scans.
 __global__ void __launch_bounds__(256) fpa_field_scan_kernel(FieldParams p) {
     __shared__ float red[4];
     const int bh = group_x(), b = bh / p.H, h = bh % p.H;
     const int tid = thread_x();
-    const int per = (p.T + 255) / 256, ta = imin(tid * per, p.T), tb = imin(ta + per, p.T);
-    const float *dl = p.lin + ((int64_t)b * p.NO + h) * p.T;
-    const float *gl = p.lin + ((int64_t)b * p.NO + p.H + h) * p.T;
-    const float *hl = p.lin + ((int64_t)b * p.NO + 2 * p.H + h) * p.T;
-    float s = 0.f;
-    for (int t = ta; t < tb; ++t) s += dl[t];
-    float run = block_scan256(s, red) - s;  // sum of the runs before this thread's
+    const float *dl = p.lin + ((int64_t)b * p.NO + h) * p.TL;
+    const float *gl = dl + (int64_t)p.H * p.TL, *hl = gl + (int64_t)p.H * p.TL;
     float *phi = p.phi + (int64_t)bh * p.T, *psi = p.psi + (int64_t)bh * p.T;
-    for (int t = ta; t < tb; ++t) {
-        run += dl[t];
-        phi[t] = run + gl[t];
-        psi[t] = run + hl[t];
+    float carry = 0.f;
+    for (int c0 = 0; c0 < p.T; c0 += 256 * SCK) {
+        float d[SCK], g[SCK], e[SCK];
+#pragma unroll
+        for (int k = 0; k < SCK; ++k) {
+            const int t = c0 + 256 * k + tid;
+            const bool ok = t < p.T;
+            d[k] = ok ? dl[t] : 0.f;
+            g[k] = ok ? gl[t] : 0.f;
+            e[k] = ok ? hl[t] : 0.f;
+        }
+#pragma unroll
+        for (int k = 0; k < SCK; ++k) {
+            const int t = c0 + 256 * k + tid;
+            float total;
+            const float run = carry + block_scan256(d[k], red, total);
+            if (t < p.T) {
+                phi[t] = run + g[k];
+                psi[t] = run + e[k];
+            }
+            carry += total;
+        }
     }
 }
 
 // Backward of the scan: d(delta)_t = sum_{u >= t} (dphi_u + dpsi_u), dg = dphi, dh = dpsi, written
-// to lin position-major, d(lin)[b][t][o], so that a position's NO values are contiguous.
+// to lin as (B, NO, TL) rows, zero past T.  Positions are taken 256 at a time from the end (thread
+// i has position c - i), so the workgroup scan runs from T down to 0; the loads of SCK chunks are
+// issued before their scans.
 __global__ void __launch_bounds__(256) fpa_field_bwd_scan_kernel(FieldParams p) {
     __shared__ float red[4];
     const int bh = group_x(), b = bh / p.H, h = bh % p.H;
     const int tid = thread_x();
-    // Thread tid takes the tid-th run counted from the end, so the scan runs from T down to 0.
-    const int per = (p.T + 255) / 256;
-    const int tb = p.T - imin(tid * per, p.T), ta = p.T - imin(tid * per + per, p.T);
     const float *dphi = p.dphi + (int64_t)bh * p.T, *dpsi = p.dpsi + (int64_t)bh * p.T;
-    float s = 0.f;
-    for (int t = tb - 1; t >= ta; --t) s += dphi[t] + dpsi[t];
-    float run = block_scan256(s, red) - s;
-    float *dl = p.lin + (int64_t)b * p.T * p.NO;  // d(lin) position-major: [b][t][o]
-    for (int t = tb - 1; t >= ta; --t) {
-        const float a = dphi[t], c = dpsi[t];
-        run += a + c;
-        dl[(int64_t)t * p.NO + h] = run;
-        dl[(int64_t)t * p.NO + p.H + h] = a;
-        dl[(int64_t)t * p.NO + 2 * p.H + h] = c;
+    float *dd = p.lin + ((int64_t)b * p.NO + h) * p.TL;
+    float *dg = dd + (int64_t)p.H * p.TL, *dh = dg + (int64_t)p.H * p.TL;
+    float carry = 0.f;
+    for (int c0 = 0; c0 < p.T; c0 += 256 * SCK) {
+        float a[SCK], c[SCK];
+#pragma unroll
+        for (int k = 0; k < SCK; ++k) {
+            const int t = p.T - 1 - c0 - 256 * k - tid;
+            a[k] = t >= 0 ? dphi[t] : 0.f;
+            c[k] = t >= 0 ? dpsi[t] : 0.f;
+        }
+#pragma unroll
+        for (int k = 0; k < SCK; ++k) {
+            const int t = p.T - 1 - c0 - 256 * k - tid;
+            float total;
+            const float run = carry + block_scan256(a[k] + c[k], red, total);
+            if (t >= 0) {
+                dd[t] = run;
+                dg[t] = a[k];
+                dh[t] = c[k];
+            }
+            carry += total;
+        }
     }
+    if (p.T + tid < p.TL) dd[p.T + tid] = dg[p.T + tid] = dh[p.T + tid] = 0.f;
 }
 
-// dx[b][t][c] = sum_o d(lin)[b][t][o] W[o][c] on the MFMA.  Grid (ceil(T / 64), B), NWF waves: the
+// dx[b][t][c] = sum_o d(lin)[b][o][t] W[o][c] on the MFMA.  Grid (ceil(T / 64), B), NWF waves: the
 // workgroup's 64 positions' gradients (NO per position, KS = NO / 2 rounded up k steps) are staged in
 // LDS once; wave w owns 32-feature N tiles [w CS, (w + 1) CS).  Per N tile and k step: A = d(lin)
 // (positions x outputs 2 ks, 2 ks + 1) from LDS, B = W rows 2 ks, 2 ks + 1 at 32 consecutive
@@ -200,8 +346,8 @@ __global__ void __launch_bounds__(64 * NWF) fpa_field_dx_kernel(FieldParams p) {
     const int w = __builtin_amdgcn_readfirstlane(tid / 64);
     const int b = group_y(), t0 = group_x() * FT;
     for (int i = tid; i < FT * 2 * KS; i += 64 * NWF) {
-        const int r = i / (2 * KS), o = i % (2 * KS);
-        dls[r][o] = (o < p.NO && t0 + r < p.T) ? p.lin[((int64_t)b * p.T + t0 + r) * p.NO + o] : 0.f;
+        const int o = i / FT, r = i % FT;
+        dls[r][o] = (o < p.NO && t0 + r < p.T) ? p.lin[((int64_t)b * p.NO + o) * p.TL + t0 + r] : 0.f;
     }
     __syncthreads();
     const int CS = ((p.C + NWF - 1) / NWF + 31) / 32 * 32;
@@ -233,12 +379,81 @@ __global__ void __launch_bounds__(64 * NWF) fpa_field_dx_kernel(FieldParams p) {
     }
 }
 
+// Four fp32 values stored as four consecutive features of dx (16 bytes in fp32, 8 in fp16).
+template <typename TX> __device__ __forceinline__ void store4(TX *a, f32x4 v);
+template <> __device__ __forceinline__ void store4<float>(float *a, f32x4 v) { *reinterpret_cast<f32x4 *>(a) = v; }
+template <> __device__ __forceinline__ void store4<f16>(f16 *a, f32x4 v) {
+    *reinterpret_cast<h4 *>(a) = __builtin_convertvector(v, h4);
+}
+
+// dx = d(lin) W on the 16x16x4 MFMA with 16-byte W loads and dx stores: needs x and dx aligned to
+// four features.  Grid (ceil(T / (16 MTD)), B), 4 waves: the workgroup's 16 MTD positions' gradients
+// (4 KS4 >= NO outputs, zero past NO and T) are staged in LDS once, [o][position]; wave w takes the
+// 64-feature N blocks w, w + 4, ...  In an N block at c0, k step m contracts outputs 4m + j over the
+// lane groups j: lane (j, r) gives A = d(lin)[4m + j][its position r] from LDS and B = W[4m + j][c0 +
+// 4r .. c0 + 4r + 3] (one 16-byte load for the four N tiles; N tile nt holds feature c0 + 4r + nt),
+// so each lane ends with four consecutive features of four positions and stores each position's as
+// one vector.  The next N block's W is loaded during the current block's products.
+template <typename TX, int KS4, int MTD>
+__global__ void __launch_bounds__(256) fpa_field_dx16_kernel(FieldParams p) {
+    constexpr int FM = 16 * MTD;
+    __shared__ float dls[4 * KS4][FM + 1];
+    const int tid = thread_x(), lane = tid % 64, j = lane / 16, r16 = lane % 16;
+    const int w = __builtin_amdgcn_readfirstlane(tid / 64);
+    const int b = group_y(), t0 = group_x() * FM;
+    for (int i = tid; i < 4 * KS4 * FM; i += 256) {
+        const int o = i / FM, r = i % FM;
+        dls[o][r] = (o < p.NO && t0 + r < p.T) ? p.lin[((int64_t)b * p.NO + o) * p.TL + t0 + r] : 0.f;
+    }
+    TX *dxb = static_cast<TX *>(p.dx) + (int64_t)b * p.sdxb;
+    const int NBK = (p.C + 63) / 64;
+    const float *wrow[KS4];  // W rows 4m + j (rows past NO read row 0; their A values are zero)
+#pragma unroll
+    for (int m = 0; m < KS4; ++m) wrow[m] = p.w + (int64_t)(4 * m + j < p.NO ? 4 * m + j : 0) * p.C;
+    auto col = [&](int nb) { const int c = nb * 64 + 4 * r16; return c < p.C ? c : p.C - 4; };
+    f32x4 wv[KS4], wn[KS4];
+    if (w < NBK) {
+        const int cl = col(w);
+#pragma unroll
+        for (int m = 0; m < KS4; ++m) wn[m] = *reinterpret_cast<const f32x4 *>(wrow[m] + cl);
+    }
+    __syncthreads();
+    for (int nb = w; nb < NBK; nb += 4) {
+#pragma unroll
+        for (int m = 0; m < KS4; ++m) wv[m] = wn[m];
+        if (nb + 4 < NBK) {
+            const int cl = col(nb + 4);
+#pragma unroll
+            for (int m = 0; m < KS4; ++m) wn[m] = *reinterpret_cast<const f32x4 *>(wrow[m] + cl);
+        }
+        const int c = nb * 64 + 4 * r16;
+#pragma unroll
+        for (int mt = 0; mt < MTD; ++mt) {
+            const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+            f32x4 acc[4] = {z4, z4, z4, z4};
+#pragma unroll
+            for (int m = 0; m < KS4; ++m) {
+                const float a = dls[4 * m + j][16 * mt + r16];
+#pragma unroll
+                for (int nt = 0; nt < 4; ++nt) acc[nt] = mma16_f32(a, wv[m][nt], acc[nt]);
+            }
+            if (c < p.C) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int t = t0 + 16 * mt + 4 * j + r;
+                    if (t < p.T) store4<TX>(dxb + (int64_t)t * p.sdxt + c, f32x4{acc[0][r], acc[1][r], acc[2][r], acc[3][r]});
+                }
+            }
+        }
+    }
+}
+
 // Partial dW and dbias over one split of the B*T positions on the MFMA: part[s][o][c] = sum_{n in
 // split s} d(lin)[n][o] x[n][c] for c < C, and the same with x = 1 at c = C (the bias).  Grid
 // (ceil((C + 1) / 64), S), 4 waves, each a quarter of the split's positions; per k step two
-// positions (lanes 0-31: n, lanes 32-63: n + 1): A = d(lin)^T (outputs x positions, 128-byte rows
-// of the position-major gradient), B = x (positions x 64 features, two N tiles).  The four
-// quarters meet in LDS in wave order.
+// positions (lanes 0-31: n, lanes 32-63: n + 1): A = d(lin)^T (outputs x positions), B = x
+// (positions x 64 features, two N tiles), one element per lane and operand.  The four quarters meet
+// in LDS in wave order.  (Any x layout; fpa_field_dw16_kernel takes four-feature-aligned x.)
 template <typename TX, int MT>
 __global__ void __launch_bounds__(256) fpa_field_dw_kernel(FieldParams p) {
     constexpr int NOP = 32 * MT, RP = 64 + 1;
@@ -267,7 +482,7 @@ __global__ void __launch_bounds__(256) fpa_field_dw_kernel(FieldParams p) {
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
                     const int o = 32 * mt + c32;
-                    av[u][mt] = (nv && o < p.NO) ? p.lin[(int64_t)n * p.NO + o] : 0.f;
+                    av[u][mt] = (nv && o < p.NO) ? p.lin[((int64_t)bl * p.NO + o) * p.TL + tl] : 0.f;
                 }
 #pragma unroll
                 for (int nt = 0; nt < 2; ++nt) {
@@ -303,6 +518,102 @@ __global__ void __launch_bounds__(256) fpa_field_dw_kernel(FieldParams p) {
         p.part[((int64_t)s * p.NO + o) * (p.C + 1) + c] = (red[0][o][lane] + red[1][o][lane]) + (red[2][o][lane] + red[3][o][lane]);
 }
 
+// Partial dW and dbias over one split of the positions on the 16x16x4 MFMA, both operands loaded
+// straight from memory: needs x aligned to four features (as the 16x16 projection).  The positions
+// are taken in groups of 16 inside one batch (a batch's TL-long rows of d(lin) are zero past T, and x
+// rows past T read row T - 1); split s takes groups [s GS, (s + 1) GS) of the B TL / 16 and wave w a
+// quarter of them.  Grid (ceil(C / 64), S), 4 waves; M = outputs (NT tiles), N = the workgroup's 64
+// features.  In a group at t0, k step j of the MFMA contracts positions t0 + 4j + s over the four
+// sub-steps s, and lane (j, r) loads d(lin)[o][t0 + 4j .. t0 + 4j + 3] for each of its outputs
+// o = 16 mt + r (A, one value per sub-step) and x[t0 + 4j + s][c0 + 4r .. c0 + 4r + 3] for each s
+// (B: feature c0 + 4r + nt in N tile nt): every load is 16 contiguous bytes and feeds four MFMAs.
+// Loads run PD groups ahead, unconditionally (as in the projection), so the waits count them
+// exactly.  dbias adds up the A values on the VALU.  The four waves meet in LDS in wave order, and
+// part[s][o][c] has the layout of fpa_field_dw_kernel's (the bias at c = C, from workgroup 0).
+template <typename TX, int NT, int PD>
+__global__ void __launch_bounds__(256) fpa_field_dw16_kernel(FieldParams p) {
+    constexpr int NOP = 16 * NT, RP = 64 + 1;
+    __shared__ float red[4][NOP][RP];
+    __shared__ float bred[4][4][NOP];  // dbias: [wave][k group][output]
+    const int tid = thread_x(), lane = tid % 64, j = lane / 16, r16 = lane % 16;
+    const int w = __builtin_amdgcn_readfirstlane(tid / 64);
+    const int c0 = group_x() * 64, s = group_y();
+    const int GB = p.TL / 16, G = p.B * GB;  // groups per batch, in all
+    const int per = (G + p.S - 1) / p.S, q = (per + 3) / 4;
+    const int lim = umin_i(s * per + per, G);
+    const int ga = umin_i(s * per + w * q, lim), gb = umin_i(ga + q, lim);
+    const int cx = c0 + 4 * r16 < p.C ? c0 + 4 * r16 : p.C - 4;  // columns past C are not stored
+    const TX *xcol = static_cast<const TX *>(p.x) + cx;
+    int orow[NT];  // d(lin) row offsets within a batch; rows past NO read row 0 and are not stored
+#pragma unroll
+    for (int mt = 0; mt < NT; ++mt) orow[mt] = (16 * mt + r16 < p.NO ? 16 * mt + r16 : 0) * p.TL + 4 * j;
+    const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+    f32x4 xv[PD][4], dv[PD][NT], acc[NT][4], bacc[NT];
+#pragma unroll
+    for (int mt = 0; mt < NT; ++mt) {
+        bacc[mt] = z4;
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = z4;
+    }
+    auto load = [&](f32x4 (&xg)[4], f32x4 (&dg)[NT], int g) {
+        const int b = g / GB, t0 = (g % GB) * 16;
+        const TX *xb = xcol + (int64_t)b * p.sxb;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int t = t0 + 4 * j + e;
+            xg[e] = load4<TX>(xb + (int64_t)(t < p.T ? t : p.T - 1) * p.sxt);
+        }
+        const float *db = p.lin + (int64_t)b * p.NO * p.TL + t0;
+#pragma unroll
+        for (int mt = 0; mt < NT; ++mt) dg[mt] = *reinterpret_cast<const f32x4 *>(db + orow[mt]);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto step = [&](const f32x4 (&xg)[4], const f32x4 (&dg)[NT]) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int mt = 0; mt < NT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = mma16_f32(dg[mt][e], xg[e][nt], acc[mt][nt]);
+#pragma unroll
+        for (int mt = 0; mt < NT; ++mt) bacc[mt] += dg[mt];
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    const int n = gb - ga;
+    if (n > 0) {
+        const int glast = gb - 1;
+#pragma unroll
+        for (int u = 0; u < PD; ++u) load(xv[u], dv[u], umin_i(ga + u, glast));
+        for (int s0 = 0; s0 < n; s0 += PD) {
+#pragma unroll
+            for (int u = 0; u < PD; ++u) {
+                if (s0 + u < n) step(xv[u], dv[u]);
+                load(xv[u], dv[u], umin_i(ga + s0 + u + PD, glast));
+            }
+        }
+    }
+#pragma unroll
+    for (int mt = 0; mt < NT; ++mt) {
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[w][16 * mt + 4 * j + r][4 * r16 + nt] = acc[mt][nt][r];
+        bred[w][j][16 * mt + r16] = (bacc[mt][0] + bacc[mt][1]) + (bacc[mt][2] + bacc[mt][3]);
+    }
+    __syncthreads();
+    for (int i = tid; i < p.NO * 64; i += 256) {
+        const int o = i / 64, cc = i % 64, c = c0 + cc;
+        if (c < p.C)
+            p.part[((int64_t)s * p.NO + o) * (p.C + 1) + c] = (red[0][o][cc] + red[1][o][cc]) + (red[2][o][cc] + red[3][o][cc]);
+    }
+    if (group_x() == 0 && tid < p.NO) {
+        float v = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v += (bred[k][0][tid] + bred[k][1][tid]) + (bred[k][2][tid] + bred[k][3][tid]);
+        p.part[((int64_t)s * p.NO + tid) * (p.C + 1) + p.C] = v;
+    }
+}
+
 // dW[o][c] (c < C) and dbias[o] (c = C) = sum_s part[s][o][c] in a fixed order: 256 threads take 64
 // entries, wave w the splits s = w mod 4, and the four wave sums are added in wave order.
 __global__ void __launch_bounds__(256) fpa_field_reduce_kernel(FieldParams p) {
@@ -311,8 +622,16 @@ __global__ void __launch_bounds__(256) fpa_field_reduce_kernel(FieldParams p) {
     const int64_t i = (int64_t)group_x() * 64 + lane;
     const int64_t C1 = p.C + 1, n = p.NO * C1;
     float a = 0.f;
-    if (i < n)
-        for (int s = w; s < p.S; s += 4) a += p.part[(int64_t)s * n + i];
+    if (i < n) {
+        // Eight splits' loads at a time, then added in split order.
+        for (int s0 = w; s0 < p.S; s0 += 32) {
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = s0 + 4 * k < p.S ? p.part[(int64_t)(s0 + 4 * k) * n + i] : 0.f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) a += v[k];
+        }
+    }
     red[w][lane] = a;
     __syncthreads();
     if (w != 0 || i >= n) return;
@@ -326,10 +645,32 @@ __global__ void __launch_bounds__(256) fpa_field_reduce_kernel(FieldParams p) {
 
 // ---------------------------------------------------------------------------------------------
 
+// x and W in four-feature units: the unit-stride loads of the 16x16 projection are aligned.
+template <typename TX>
+static bool four_feature_aligned(const FieldParams &p) {
+    const uintptr_t ax = reinterpret_cast<uintptr_t>(p.x), aw = reinterpret_cast<uintptr_t>(p.w);
+    return p.C % 4 == 0 && p.sxt % 4 == 0 && p.sxb % 4 == 0 && ax % (4 * sizeof(TX)) == 0 && aw % 16 == 0;
+}
+
+// The same for dx (the backward's 16x16 kernels read x and write dx in four-feature vectors).
+template <typename TX>
+static bool dx_four_feature_aligned(const FieldParams &p) {
+    const uintptr_t ad = reinterpret_cast<uintptr_t>(p.dx);
+    return four_feature_aligned<TX>(p) && p.sdxt % 4 == 0 && p.sdxb % 4 == 0 && ad % (4 * sizeof(TX)) == 0;
+}
+
 template <typename TX>
 static hipError_t field_fwd_t(const FieldParams &p, hipStream_t s) {
     const dim3 grid((p.T + FT - 1) / FT, p.B);
-    if (p.NO <= 32) hipLaunchKernelGGL((fpa_field_proj_kernel<TX, 1, 8>), grid, dim3(512), 0, s, p);
+    if (four_feature_aligned<TX>(p)) {
+        constexpr int MT = 4, PD = 3, LG = 1;
+        const dim3 g16((p.T + 16 * MT - 1) / (16 * MT), p.B);
+        if (p.NO <= 16) hipLaunchKernelGGL((fpa_field_proj16_kernel<TX, 1, 8, PD, MT, LG>), g16, dim3(512), 0, s, p);
+        else if (p.NO <= 32) hipLaunchKernelGGL((fpa_field_proj16_kernel<TX, 2, 8, PD, MT, LG>), g16, dim3(512), 0, s, p);
+        else if (p.NO <= 48) hipLaunchKernelGGL((fpa_field_proj16_kernel<TX, 3, 8, PD, MT, LG>), g16, dim3(512), 0, s, p);
+        else if (p.NO <= 64) hipLaunchKernelGGL((fpa_field_proj16_kernel<TX, 4, 4, PD, MT, LG>), g16, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((fpa_field_proj16_kernel<TX, 6, 4, PD, MT, LG>), g16, dim3(256), 0, s, p);
+    } else if (p.NO <= 32) hipLaunchKernelGGL((fpa_field_proj_kernel<TX, 1, 8>), grid, dim3(512), 0, s, p);
     else if (p.NO <= 64) hipLaunchKernelGGL((fpa_field_proj_kernel<TX, 2, 8>), grid, dim3(512), 0, s, p);
     else hipLaunchKernelGGL((fpa_field_proj_kernel<TX, 3, 4>), grid, dim3(256), 0, s, p);
     hipError_t e = hipGetLastError();
@@ -343,7 +684,16 @@ static hipError_t field_bwd_t(const FieldParams &p, hipStream_t s) {
     hipLaunchKernelGGL(fpa_field_bwd_scan_kernel, dim3(p.B * p.H), dim3(256), 0, s, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    if (p.dx != nullptr) {
+    if (p.dx != nullptr && dx_four_feature_aligned<TX>(p)) {
+        constexpr int MTD = 4;
+        const dim3 grid((p.T + 16 * MTD - 1) / (16 * MTD), p.B);
+        if (p.NO <= 12) hipLaunchKernelGGL((fpa_field_dx16_kernel<TX, 3, MTD>), grid, dim3(256), 0, s, p);
+        else if (p.NO <= 24) hipLaunchKernelGGL((fpa_field_dx16_kernel<TX, 6, MTD>), grid, dim3(256), 0, s, p);
+        else if (p.NO <= 36) hipLaunchKernelGGL((fpa_field_dx16_kernel<TX, 9, MTD>), grid, dim3(256), 0, s, p);
+        else if (p.NO <= 48) hipLaunchKernelGGL((fpa_field_dx16_kernel<TX, 12, MTD>), grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((fpa_field_dx16_kernel<TX, 24, MTD>), grid, dim3(256), 0, s, p);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    } else if (p.dx != nullptr) {
         const dim3 grid((p.T + FT - 1) / FT, p.B);
         if (p.NO <= 12) hipLaunchKernelGGL((fpa_field_dx_kernel<TX, 6, 8>), grid, dim3(512), 0, s, p);
         else if (p.NO <= 24) hipLaunchKernelGGL((fpa_field_dx_kernel<TX, 12, 8>), grid, dim3(512), 0, s, p);
@@ -352,10 +702,20 @@ static hipError_t field_bwd_t(const FieldParams &p, hipStream_t s) {
         else hipLaunchKernelGGL((fpa_field_dx_kernel<TX, 48, 4>), grid, dim3(256), 0, s, p);  // registers
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    const dim3 gw((p.C + 1 + 63) / 64, p.S);
-    if (p.NO <= 32) hipLaunchKernelGGL((fpa_field_dw_kernel<TX, 1>), gw, dim3(256), 0, s, p);
-    else if (p.NO <= 64) hipLaunchKernelGGL((fpa_field_dw_kernel<TX, 2>), gw, dim3(256), 0, s, p);
-    else hipLaunchKernelGGL((fpa_field_dw_kernel<TX, 3>), gw, dim3(256), 0, s, p);
+    if (four_feature_aligned<TX>(p)) {
+        constexpr int PD = 2;
+        const dim3 gw((p.C + 63) / 64, p.S);
+        if (p.NO <= 16) hipLaunchKernelGGL((fpa_field_dw16_kernel<TX, 1, PD>), gw, dim3(256), 0, s, p);
+        else if (p.NO <= 32) hipLaunchKernelGGL((fpa_field_dw16_kernel<TX, 2, PD>), gw, dim3(256), 0, s, p);
+        else if (p.NO <= 48) hipLaunchKernelGGL((fpa_field_dw16_kernel<TX, 3, PD>), gw, dim3(256), 0, s, p);
+        else if (p.NO <= 64) hipLaunchKernelGGL((fpa_field_dw16_kernel<TX, 4, PD>), gw, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((fpa_field_dw16_kernel<TX, 6, PD>), gw, dim3(256), 0, s, p);
+    } else {
+        const dim3 gw((p.C + 1 + 63) / 64, p.S);
+        if (p.NO <= 32) hipLaunchKernelGGL((fpa_field_dw_kernel<TX, 1>), gw, dim3(256), 0, s, p);
+        else if (p.NO <= 64) hipLaunchKernelGGL((fpa_field_dw_kernel<TX, 2>), gw, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((fpa_field_dw_kernel<TX, 3>), gw, dim3(256), 0, s, p);
+    }
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(fpa_field_reduce_kernel, dim3((p.NO * (p.C + 1) + 63) / 64), dim3(256), 0, s, p);
     return hipGetLastError();

@@ -66,12 +66,13 @@ struct FieldParams {
     void *dx; int64_t sdxb, sdxt;       // backward: x's dtype and layout rules (NULL: not computed)
     const float *w;                     // (NO, C) row-major
     const float *bias;                  // (NO,)
-    float *lin;                         // the projection (B, NO, T), or in the backward its gradient (B, T, NO)
+    float *lin;                         // the projection, or in the backward its gradient: (B, NO, TL)
     float *phi, *psi;                   // (B, H, T) contiguous
     const float *dphi, *dpsi;           // (B, H, T) contiguous
     float *dw, *dbias;                  // (NO, C), (NO,)
     float *part;                        // (S, NO, C + 1): dW and dbias partials over S splits of the B*T positions
     int B, T, C, H, NO, S;              // NO = 3H
+    int TL;                             // lin's row length: T rounded up to 16 (the gradient is zero past T)
 };
 
 // BwdParams::qinfo holds, per 64-query block of a head, QI_PLANES planes of 64 floats

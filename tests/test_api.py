@@ -242,12 +242,14 @@ def test_field_c_abi_validation(field, value, code, msg):
 
 
 def test_field_workspace_size():
-    """The projection as B*3H*T floats plus the dW / dbias partials (at most 64 splits of the positions)."""
+    """The projection as B*3H rows of T rounded up to 16 floats, plus the dW / dbias partials (at most
+    64 splits of the positions)."""
     L = _lib.lib()
-    B, T, C, H = 8, 2048, 768, 12
-    S = min(64, (B * T + 255) // 256)
     up = lambda n: (n + 63) // 64 * 64
-    assert L.fpa_field_workspace_bytes(B, T, C, H) == 4 * (up(B * 3 * H * T + 96) + up(S * 3 * H * (C + 1)))
+    for B, T, C, H in ((8, 2048, 768, 12), (3, 257, 70, 5), (1, 1, 16, 1)):
+        S = min(64, (B * T + 255) // 256)
+        TL = (T + 15) // 16 * 16
+        assert L.fpa_field_workspace_bytes(B, T, C, H) == 4 * (up(B * 3 * H * TL) + up(S * 3 * H * (C + 1)))
 
 
 def test_library_is_built_from_these_sources():
