@@ -55,6 +55,10 @@ def _case(hip, x, H, seed):
     (3, 257, 70, 5, torch.float32),
     (2, 300, 96, 12, torch.float16),
     (1, 64, 768, 32, torch.float32),
+    (2, 45, 70, 3, torch.float16),     # C not a multiple of 4: the one-element-per-lane kernels in fp16
+    (2, 33, 20, 6, torch.float32),     # C = 20: a last projection step of 4 features
+    (3, 50, 36, 2, torch.float32),     # C = 36: waves with 16, 16 and 4 features
+    (1, 200, 768, 32, torch.float16),  # 96 outputs: six 16-wide tiles in fp16
 ])
 def test_field_matches_the_definition(hip, B, T, C, H, dtype):
     _say(f"[field] B{B} T{T} C{C} H{H} {dtype}")
@@ -65,6 +69,28 @@ def test_field_matches_the_definition(hip, B, T, C, H, dtype):
         assert torch.isfinite(a).all(), name
         tol = 2e-3 if (name == "dx" and dtype == torch.float16) else 1e-5
         assert _rel(a, r) <= tol, (name, _rel(a, r))
+
+
+@pytest.mark.parametrize("C", [64, 70])
+def test_field_without_dx(hip, C):
+    """x that needs no gradient: the backward skips dx (a NULL dx in the C ABI) and still gives dW
+    and dbias, for aligned (C = 64) and unaligned (C = 70) features."""
+    _say(f"[field] no dx, C={C}")
+    B, T, H = 2, 90, 4
+    g = torch.Generator().manual_seed(C)
+    x = torch.randn(B, T, C, generator=g)
+    w = torch.randn(3 * H, C, generator=g) / C ** 0.5
+    b = torch.randn(3 * H, generator=g)
+    dphi, dpsi = torch.randn(B, H, T, generator=g), torch.randn(B, H, T, generator=g)
+    dev = "cuda"
+    wd, bd = w.to(dev).requires_grad_(), b.to(dev).requires_grad_()
+    phi, psi = hip.FieldHIP.apply(x.to(dev), wd, bd, H)
+    dw, db = torch.autograd.grad((phi, psi), (wd, bd), (dphi.to(dev), dpsi.to(dev)))
+    wr, br = w.double().requires_grad_(), b.double().requires_grad_()
+    rphi, rpsi = O.field_phi_psi(x.double(), wr, br, H)
+    rdw, rdb = torch.autograd.grad((rphi, rpsi), (wr, br), (dphi.double(), dpsi.double()))
+    for name, a, r in (("phi", phi, rphi.detach()), ("psi", psi, rpsi.detach()), ("dW", dw, rdw), ("dbias", db, rdb)):
+        assert _rel(a, r) <= 1e-5, (name, _rel(a, r))
 
 
 def test_field_strided_x_and_determinism(hip):
