@@ -7,10 +7,10 @@
 //
 // The projection has only 3H outputs per position (36 for H = 12), so it is a pass over x
 // (HBM-bound) with little arithmetic, done on the fp32 MFMA (the reference computes it in fp32).
-// With x aligned to four features (the usual case) the 16x16x4 kernels load x, W and d(lin) as
-// 16-byte vectors straight into MFMA operands, using the freedom to order the contraction so that
-// one four-feature load feeds four MFMAs; other layouts take the 32x32x2 kernels, which read one
-// element per lane.  The projection is stored per (batch, output) along t, in rows of TL = T
+// With x aligned to four features (the usual case) the 16x16x4 kernels read x, W and d(lin) as
+// 16-byte vectors into MFMA operands (the projection, up to 48 outputs, through an LDS tile staged
+// from contiguous row pieces), using the freedom to order the contraction so that one four-feature
+// operand feeds four MFMAs; other layouts take the 32x32x2 kernels, which read one element per lane.  The projection is stored per (batch, output) along t, in rows of TL = T
 // rounded up to 16, so the cumulative sum over t reads contiguous rows.  Backward: a reverse
 // cumulative sum gives d(delta) (the gradient is stored in the same layout, zero past T); dx =
 // d(lin) W is the same pass the other way round; dW = d(lin)^T x (and dbias) is summed in a fixed
@@ -260,6 +260,110 @@ __global__ void __launch_bounds__(64 * NWF) fpa_field_proj16_kernel(FieldParams 
 }
 
 constexpr int SCK = 8;  // 256-position chunks whose loads a scan issues together
+
+// lin as fpa_field_proj16_kernel computes it (same operands and order of the contraction), with x
+// staged through LDS: 8 waves, 64 positions; the workgroup loads 128-feature chunks of its 64 rows
+// with 512 contiguous bytes per row (fp32; 256 in fp16) into a double-buffered LDS tile, the loads
+// two chunks ahead, and wave w takes features 16w .. 16w + 15 of each chunk (A operands as 16-byte
+// LDS reads, W as 16-byte loads, one chunk ahead).  One barrier per chunk; past C the tile and W
+// hold zeros.
+template <typename TX, int NT>
+__global__ void __launch_bounds__(512) fpa_field_proj_staged_kernel(FieldParams p) {
+    constexpr int NWF = 8, KC = 16 * NWF, XPS = KC + 4, NOP = 16 * NT, RP = FT + 1;
+    constexpr int STG = 2 * FT * XPS, RED = NWF * NOP * RP;
+    __shared__ __attribute__((aligned(16))) float lds[STG > RED ? STG : RED];
+    const int tid = thread_x(), lane = tid % 64, j = lane / 16, r16 = lane % 16;
+    const int w = __builtin_amdgcn_readfirstlane(tid / 64);
+    const int b = group_y(), t0 = group_x() * FT;
+    const TX *xb = static_cast<const TX *>(p.x) + (int64_t)b * p.sxb;
+    const int NCH = (p.C + KC - 1) / KC;
+    const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+    // Staging: thread tid moves rows lr + 16q (q < 4), features 4 lc .. 4 lc + 3 of a chunk; rows
+    // past T read row T - 1 (their sums are not stored).
+    const int lr = tid / 32, lc = tid % 32;
+    const TX *srow[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int t = t0 + lr + 16 * q;
+        srow[q] = xb + (int64_t)(t < p.T ? t : p.T - 1) * p.sxt;
+    }
+    f32x4 sa[4], sb[4];  // chunks ch + 1 and ch + 2 in flight, alternately in sa and sb
+    auto gload = [&](int ch, f32x4 (&sv)[4]) {
+        const int c = ch * KC + 4 * lc;
+        const int cl = c < p.C ? c : p.C - 4;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sv[q] = load4<TX>(srow[q] + cl);
+    };
+    auto lstore = [&](int ch, int buf, const f32x4 (&sv)[4]) {
+        const bool ok = ch * KC + 4 * lc < p.C;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<f32x4 *>(&lds[(buf * FT + lr + 16 * q) * XPS + 4 * lc]) = ok ? sv[q] : z4;
+    };
+    const float *wrow[NT];  // rows past NO read row 0 (their sums are not stored)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) wrow[nt] = p.w + (int64_t)(16 * nt + r16 < p.NO ? 16 * nt + r16 : 0) * p.C;
+    f32x4 wv[NT], wn[NT], acc[4][NT];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = z4;
+    auto wload = [&](int ch) {
+        const int c = ch * KC + 16 * w + 4 * j;
+        const int cl = c < p.C ? c : p.C - 4;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) wn[nt] = *reinterpret_cast<const f32x4 *>(wrow[nt] + cl);
+    };
+    // Chunk ch: compute from LDS buffer ch % 2, then stage chunk ch + 1 (loaded two chunks earlier,
+    // in sb for even ch, in sa for odd) into the other buffer and load chunk ch + 3 in its place.
+    auto chunk = [&](int ch, f32x4 (&sv)[4]) {
+        const int buf = ch & 1;
+        const bool wok = ch * KC + 16 * w + 4 * j < p.C;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) wv[nt] = wok ? wn[nt] : z4;
+        if (ch + 1 < NCH) wload(ch + 1);
+        __syncthreads();  // chunk ch is in buffer buf; buffer buf ^ 1 is no longer read
+        f32x4 xa[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+            xa[mt] = *reinterpret_cast<const f32x4 *>(&lds[(buf * FT + 16 * mt + r16) * XPS + 16 * w + 4 * j]);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = mma16_f32(xa[mt][ks], wv[nt][ks], acc[mt][nt]);
+        if (ch + 1 < NCH) {
+            lstore(ch + 1, buf ^ 1, sv);
+            if (ch + 3 < NCH) gload(ch + 3, sv);
+        }
+    };
+    gload(0, sa);
+    wload(0);
+    lstore(0, 0, sa);
+    if (NCH > 1) gload(1, sb);
+    if (NCH > 2) gload(2, sa);
+    for (int ch = 0; ch < NCH; ch += 2) {
+        chunk(ch, sb);
+        if (ch + 1 < NCH) chunk(ch + 1, sa);
+    }
+    __syncthreads();  // staging done; the same LDS takes the partial sums, [w][o][position]
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) lds[(w * NOP + 16 * nt + r16) * RP + 16 * mt + 4 * j + r] = acc[mt][nt][r];
+    __syncthreads();
+    const int t = t0 + lane;
+    if (t >= p.T) return;
+    for (int o = w; o < p.NO; o += NWF) {
+        float v = 0.f;
+#pragma unroll
+        for (int k = 0; k < NWF; ++k) v += lds[(k * NOP + o) * RP + lane];
+        p.lin[((int64_t)b * p.NO + o) * p.TL + t] = v + p.bias[o];
+    }
+}
 
 // phi = cumsum_t(delta) + g, psi = cumsum_t(delta) + h for one (b, h) per workgroup (256 threads):
 // 256 consecutive positions at a time, one per thread (coalesced rows), scanned across the
@@ -665,9 +769,9 @@ static hipError_t field_fwd_t(const FieldParams &p, hipStream_t s) {
     if (four_feature_aligned<TX>(p)) {
         constexpr int MT = 4, PD = 3, LG = 1;
         const dim3 g16((p.T + 16 * MT - 1) / (16 * MT), p.B);
-        if (p.NO <= 16) hipLaunchKernelGGL((fpa_field_proj16_kernel<TX, 1, 8, PD, MT, LG>), g16, dim3(512), 0, s, p);
-        else if (p.NO <= 32) hipLaunchKernelGGL((fpa_field_proj16_kernel<TX, 2, 8, PD, MT, LG>), g16, dim3(512), 0, s, p);
-        else if (p.NO <= 48) hipLaunchKernelGGL((fpa_field_proj16_kernel<TX, 3, 8, PD, MT, LG>), g16, dim3(512), 0, s, p);
+        if (p.NO <= 16) hipLaunchKernelGGL((fpa_field_proj_staged_kernel<TX, 1>), grid, dim3(512), 0, s, p);
+        else if (p.NO <= 32) hipLaunchKernelGGL((fpa_field_proj_staged_kernel<TX, 2>), grid, dim3(512), 0, s, p);
+        else if (p.NO <= 48) hipLaunchKernelGGL((fpa_field_proj_staged_kernel<TX, 3>), grid, dim3(512), 0, s, p);
         else if (p.NO <= 64) hipLaunchKernelGGL((fpa_field_proj16_kernel<TX, 4, 4, PD, MT, LG>), g16, dim3(256), 0, s, p);
         else hipLaunchKernelGGL((fpa_field_proj16_kernel<TX, 6, 4, PD, MT, LG>), g16, dim3(256), 0, s, p);
     } else if (p.NO <= 32) hipLaunchKernelGGL((fpa_field_proj_kernel<TX, 1, 8>), grid, dim3(512), 0, s, p);
