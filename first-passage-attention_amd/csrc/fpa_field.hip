@@ -160,21 +160,20 @@ template <> __device__ __forceinline__ f32x4 load4<f16>(const f16 *a) {
     return __builtin_convertvector(*reinterpret_cast<const h4 *>(a), f32x4);
 }
 
-// lin on the 16x16x4 MFMA, x loaded straight into A operands: needs C, x's strides and the x and W
-// pointers aligned to four features.  Grid (ceil(T / (16 MT)), B), NWF waves; wave w owns features
-// [w CS, (w + 1) CS) for the workgroup's 16 MT positions (MT M tiles) and 16 NT >= NO outputs (N
-// tiles).  Per
-// 16-feature step, lane (k group j = l / 16, row r = l % 16) loads features c + 4j .. c + 4j + 3 of
-// each of its MT positions and of each of its W rows, and k step s of the four contracts feature
-// c + 4j + s: one 4-feature load feeds four MFMAs, x is read once, and no LDS is involved.  Loads
+// lin on the 16x16x4 MFMA, x loaded straight into A operands (the path for more than 48 outputs;
+// fewer take the staged kernel below): needs C, x's strides and the x and W pointers aligned to four
+// features.  Grid (ceil(T / (16 MT)), B), NWF waves; wave w owns features [w CS, (w + 1) CS) for the
+// workgroup's 16 MT positions (MT M tiles) and 16 NT >= NO outputs (N tiles).  Per 16-feature step,
+// lane (k group j = l / 16, row r = l % 16) loads features c + 4j .. c + 4j + 3 of each of its MT
+// positions and of each of its W rows, and k step s of the four contracts feature c + 4j + s: one
+// 4-feature load feeds four MFMAs, x is read once, and the operands do not pass through LDS.  Loads
 // run PD steps ahead in a ring of registers; nothing is done to the loaded values before their
 // MFMAs (rows past T or NO read an in-bounds row, and only give sums that are never stored), so
 // the waits for a step's loads fall just before its products.  A last step of 4, 8 or 12 features
 // (C not a multiple of 16) zeroes the W values past the wave's features.  The NWF partial sums of
 // a position meet in LDS and are added in wave order.
-template <typename TX, int NT, int NWF, int PD, int MT, int LG>
+template <typename TX, int NT, int NWF, int PD, int MT>
 __global__ void __launch_bounds__(64 * NWF) fpa_field_proj16_kernel(FieldParams p) {
-    static_assert(PD % LG == 0, "loads are issued LG steps at a time");
     constexpr int NOP = 16 * NT, FM = 16 * MT, RP = FM + 1;
     __shared__ float red[NWF * NOP * RP];
     const int tid = thread_x(), lane = tid % 64, j = lane / 16, r16 = lane % 16;
@@ -226,12 +225,9 @@ __global__ void __launch_bounds__(64 * NWF) fpa_field_proj16_kernel(FieldParams 
         for (int u = 0; u < PD; ++u) load(xr[u], wr[u], umin_i(ca + 16 * u, clast));
         for (int s0 = 0; s0 < nfull; s0 += PD) {
 #pragma unroll
-            for (int h = 0; h < PD; h += LG) {
-#pragma unroll
-                for (int u = h; u < h + LG; ++u)
-                    if (s0 + u < nfull) step(xr[u], wr[u]);
-#pragma unroll
-                for (int u = h; u < h + LG; ++u) load(xr[u], wr[u], umin_i(ca + 16 * (s0 + u + PD), clast));
+            for (int u = 0; u < PD; ++u) {
+                if (s0 + u < nfull) step(xr[u], wr[u]);
+                load(xr[u], wr[u], umin_i(ca + 16 * (s0 + u + PD), clast));
             }
         }
     }
@@ -767,13 +763,13 @@ template <typename TX>
 static hipError_t field_fwd_t(const FieldParams &p, hipStream_t s) {
     const dim3 grid((p.T + FT - 1) / FT, p.B);
     if (four_feature_aligned<TX>(p)) {
-        constexpr int MT = 4, PD = 3, LG = 1;
+        constexpr int MT = 4, PD = 3;
         const dim3 g16((p.T + 16 * MT - 1) / (16 * MT), p.B);
         if (p.NO <= 16) hipLaunchKernelGGL((fpa_field_proj_staged_kernel<TX, 1>), grid, dim3(512), 0, s, p);
         else if (p.NO <= 32) hipLaunchKernelGGL((fpa_field_proj_staged_kernel<TX, 2>), grid, dim3(512), 0, s, p);
         else if (p.NO <= 48) hipLaunchKernelGGL((fpa_field_proj_staged_kernel<TX, 3>), grid, dim3(512), 0, s, p);
-        else if (p.NO <= 64) hipLaunchKernelGGL((fpa_field_proj16_kernel<TX, 4, 4, PD, MT, LG>), g16, dim3(256), 0, s, p);
-        else hipLaunchKernelGGL((fpa_field_proj16_kernel<TX, 6, 4, PD, MT, LG>), g16, dim3(256), 0, s, p);
+        else if (p.NO <= 64) hipLaunchKernelGGL((fpa_field_proj16_kernel<TX, 4, 4, PD, MT>), g16, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((fpa_field_proj16_kernel<TX, 6, 4, PD, MT>), g16, dim3(256), 0, s, p);
     } else if (p.NO <= 32) hipLaunchKernelGGL((fpa_field_proj_kernel<TX, 1, 8>), grid, dim3(512), 0, s, p);
     else if (p.NO <= 64) hipLaunchKernelGGL((fpa_field_proj_kernel<TX, 2, 8>), grid, dim3(512), 0, s, p);
     else hipLaunchKernelGGL((fpa_field_proj_kernel<TX, 3, 4>), grid, dim3(256), 0, s, p);
