@@ -33,7 +33,10 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_prep_kernel(BwdParams p) {
     if (ok) {
         const T *Or = static_cast<const T *>(p.o) + b * p.so.b + h * p.so.h + (int64_t)row * p.so.t;
         const T *Dr = static_cast<const T *>(p.dout) + b * p.sdo.b + h * p.sdo.h + (int64_t)row * p.sdo.t;
-        for (int cc = part; cc < CPR; cc += 4) {
+#pragma unroll
+        for (int i = 0; i < (CPR + 3) / 4; ++i) {  // unrolled: every chunk's loads issued together
+            const int cc = part + 4 * i;
+            if (cc >= CPR) break;
             if constexpr (sizeof(T) == 2) {
                 h8 ov = *reinterpret_cast<const h8 *>(Or + cc * CE);
                 h8 dv = *reinterpret_cast<const h8 *>(Dr + cc * CE);
