@@ -494,13 +494,13 @@ template <> __device__ __forceinline__ void store4<f16>(f16 *a, f32x4 v) {
 // 4r .. c0 + 4r + 3] (one 16-byte load for the four N tiles; N tile nt holds feature c0 + 4r + nt),
 // so each lane ends with four consecutive features of four positions and stores each position's as
 // one vector.  The next N block's W is loaded during the current block's products.
+// Workgroup (gx, gy) = (position tile, batch); dls is LDS of 4 KS4 rows.
 template <typename TX, int KS4, int MTD>
-__global__ void __launch_bounds__(256) fpa_field_dx16_kernel(FieldParams p) {
+__device__ __forceinline__ void field_dx16(const FieldParams &p, int gx, int gy, float (*dls)[16 * MTD + 1]) {
     constexpr int FM = 16 * MTD;
-    __shared__ float dls[4 * KS4][FM + 1];
     const int tid = thread_x(), lane = tid % 64, j = lane / 16, r16 = lane % 16;
     const int w = __builtin_amdgcn_readfirstlane(tid / 64);
-    const int b = group_y(), t0 = group_x() * FM;
+    const int b = gy, t0 = gx * FM;
     for (int i = tid; i < 4 * KS4 * FM; i += 256) {
         const int o = i / FM, r = i % FM;
         dls[o][r] = (o < p.NO && t0 + r < p.T) ? p.lin[((int64_t)b * p.NO + o) * p.TL + t0 + r] : 0.f;
@@ -630,14 +630,15 @@ __global__ void __launch_bounds__(256) fpa_field_dw_kernel(FieldParams p) {
 // Loads run PD groups ahead, unconditionally (as in the projection), so the waits count them
 // exactly.  dbias adds up the A values on the VALU.  The four waves meet in LDS in wave order, and
 // part[s][o][c] has the layout of fpa_field_dw_kernel's (the bias at c = C, from workgroup 0).
+// Workgroup (gx, gy) = (feature block, split); red and bred are LDS ([4][16 NT][65] and, for dbias,
+// [wave][k group][output]).
 template <typename TX, int NT, int PD>
-__global__ void __launch_bounds__(256) fpa_field_dw16_kernel(FieldParams p) {
-    constexpr int NOP = 16 * NT, RP = 64 + 1;
-    __shared__ float red[4][NOP][RP];
-    __shared__ float bred[4][4][NOP];  // dbias: [wave][k group][output]
+__device__ __forceinline__ void field_dw16(const FieldParams &p, int gx, int gy, float (*red)[16 * NT][65],
+                                           float (*bred)[4][16 * NT]) {
+    constexpr int NOP = 16 * NT;
     const int tid = thread_x(), lane = tid % 64, j = lane / 16, r16 = lane % 16;
     const int w = __builtin_amdgcn_readfirstlane(tid / 64);
-    const int c0 = group_x() * 64, s = group_y();
+    const int c0 = gx * 64, s = gy;
     const int GB = p.TL / 16, G = p.B * GB;  // groups per batch, in all
     const int per = (G + p.S - 1) / p.S, q = (per + 3) / 4;
     const int lim = umin_i(s * per + per, G);
@@ -706,11 +707,36 @@ __global__ void __launch_bounds__(256) fpa_field_dw16_kernel(FieldParams p) {
         if (c < p.C)
             p.part[((int64_t)s * p.NO + o) * (p.C + 1) + c] = (red[0][o][cc] + red[1][o][cc]) + (red[2][o][cc] + red[3][o][cc]);
     }
-    if (group_x() == 0 && tid < p.NO) {
+    if (gx == 0 && tid < p.NO) {
         float v = 0.f;
 #pragma unroll
         for (int k = 0; k < 4; ++k) v += (bred[k][0][tid] + bred[k][1][tid]) + (bred[k][2][tid] + bred[k][3][tid]);
         p.part[((int64_t)s * p.NO + tid) * (p.C + 1) + p.C] = v;
+    }
+}
+
+template <typename TX, int NT, int PD>
+__global__ void __launch_bounds__(256) fpa_field_dw16_kernel(FieldParams p) {
+    __shared__ float red[4][16 * NT][65];
+    __shared__ float bred[4][4][16 * NT];
+    field_dw16<TX, NT, PD>(p, group_x(), group_y(), red, bred);
+}
+
+// dx and the dW partials in one launch, so that the two passes share the chip (dx has one wave per
+// SIMD alone): a 1-D grid of the dx workgroups first (the longer ones), then the dW workgroups, over
+// one LDS area that either kind uses as its own.
+template <typename TX, int KS4, int NT>
+__global__ void __launch_bounds__(256) fpa_field_dxdw_kernel(FieldParams p) {
+    constexpr int MTD = 4, FM = 16 * MTD;
+    constexpr int DXF = 4 * KS4 * (FM + 1), DWF = 4 * 16 * NT * 65 + 4 * 4 * 16 * NT;
+    __shared__ __attribute__((aligned(16))) float lds[DXF > DWF ? DXF : DWF];
+    const int ntb = (p.T + FM - 1) / FM, ndx = ntb * p.B, id = group_x();
+    if (id < ndx) {
+        field_dx16<TX, KS4, MTD>(p, id % ntb, id / ntb, reinterpret_cast<float (*)[FM + 1]>(lds));
+    } else {
+        const int k = id - ndx, nbx = (p.C + 63) / 64;
+        field_dw16<TX, NT, 2>(p, k % nbx, k / nbx, reinterpret_cast<float (*)[16 * NT][65]>(lds),
+                              reinterpret_cast<float (*)[4][16 * NT]>(lds + 4 * 16 * NT * 65));
     }
 }
 
@@ -784,16 +810,21 @@ static hipError_t field_bwd_t(const FieldParams &p, hipStream_t s) {
     hipLaunchKernelGGL(fpa_field_bwd_scan_kernel, dim3(p.B * p.H), dim3(256), 0, s, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    if (p.dx != nullptr && dx_four_feature_aligned<TX>(p)) {
-        constexpr int MTD = 4;
-        const dim3 grid((p.T + 16 * MTD - 1) / (16 * MTD), p.B);
-        if (p.NO <= 12) hipLaunchKernelGGL((fpa_field_dx16_kernel<TX, 3, MTD>), grid, dim3(256), 0, s, p);
-        else if (p.NO <= 24) hipLaunchKernelGGL((fpa_field_dx16_kernel<TX, 6, MTD>), grid, dim3(256), 0, s, p);
-        else if (p.NO <= 36) hipLaunchKernelGGL((fpa_field_dx16_kernel<TX, 9, MTD>), grid, dim3(256), 0, s, p);
-        else if (p.NO <= 48) hipLaunchKernelGGL((fpa_field_dx16_kernel<TX, 12, MTD>), grid, dim3(256), 0, s, p);
-        else hipLaunchKernelGGL((fpa_field_dx16_kernel<TX, 24, MTD>), grid, dim3(256), 0, s, p);
+    if (p.dx != nullptr && dx_four_feature_aligned<TX>(p)) {  // dx and dW partials in one launch
+        const dim3 grid(((p.T + 63) / 64) * p.B + ((p.C + 63) / 64) * p.S);
+        if (p.NO <= 12) hipLaunchKernelGGL((fpa_field_dxdw_kernel<TX, 3, 1>), grid, dim3(256), 0, s, p);
+        else if (p.NO <= 16) hipLaunchKernelGGL((fpa_field_dxdw_kernel<TX, 6, 1>), grid, dim3(256), 0, s, p);
+        else if (p.NO <= 24) hipLaunchKernelGGL((fpa_field_dxdw_kernel<TX, 6, 2>), grid, dim3(256), 0, s, p);
+        else if (p.NO <= 32) hipLaunchKernelGGL((fpa_field_dxdw_kernel<TX, 9, 2>), grid, dim3(256), 0, s, p);
+        else if (p.NO <= 36) hipLaunchKernelGGL((fpa_field_dxdw_kernel<TX, 9, 3>), grid, dim3(256), 0, s, p);
+        else if (p.NO <= 48) hipLaunchKernelGGL((fpa_field_dxdw_kernel<TX, 12, 3>), grid, dim3(256), 0, s, p);
+        else if (p.NO <= 64) hipLaunchKernelGGL((fpa_field_dxdw_kernel<TX, 24, 4>), grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((fpa_field_dxdw_kernel<TX, 24, 6>), grid, dim3(256), 0, s, p);
         if ((e = hipGetLastError()) != hipSuccess) return e;
-    } else if (p.dx != nullptr) {
+        hipLaunchKernelGGL(fpa_field_reduce_kernel, dim3((p.NO * (p.C + 1) + 63) / 64), dim3(256), 0, s, p);
+        return hipGetLastError();
+    }
+    if (p.dx != nullptr) {
         const dim3 grid((p.T + FT - 1) / FT, p.B);
         if (p.NO <= 12) hipLaunchKernelGGL((fpa_field_dx_kernel<TX, 6, 8>), grid, dim3(512), 0, s, p);
         else if (p.NO <= 24) hipLaunchKernelGGL((fpa_field_dx_kernel<TX, 12, 8>), grid, dim3(512), 0, s, p);
