@@ -257,12 +257,13 @@ __global__ void __launch_bounds__(64 * NWF) fpa_field_proj16_kernel(FieldParams 
 
 constexpr int SCK = 8;  // 256-position chunks whose loads a scan issues together
 
-// lin as fpa_field_proj16_kernel computes it (same operands and order of the contraction), with x
-// staged through LDS: 8 waves, 64 positions; the workgroup loads 128-feature chunks of its 64 rows
+// lin with the operand layout of fpa_field_proj16_kernel, x staged through LDS (up to 48 outputs):
+// 8 waves, 64 positions; the workgroup loads 128-feature chunks of its 64 rows
 // with 512 contiguous bytes per row (fp32; 256 in fp16) into a double-buffered LDS tile, the loads
 // two chunks ahead, and wave w takes features 16w .. 16w + 15 of each chunk (A operands as 16-byte
 // LDS reads, W as 16-byte loads, one chunk ahead).  One barrier per chunk; past C the tile and W
-// hold zeros.
+// hold zeros.  Each wave's partial sums (its slices of every chunk, in chunk order) are added in
+// wave order, so reruns are bit-identical.
 template <typename TX, int NT>
 __global__ void __launch_bounds__(512) fpa_field_proj_staged_kernel(FieldParams p) {
     constexpr int NWF = 8, KC = 16 * NWF, XPS = KC + 4, NOP = 16 * NT, RP = FT + 1;
