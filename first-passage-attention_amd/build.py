@@ -49,9 +49,24 @@ def _srchash():
     return mod.source_hash()
 
 
+def _extra_flags():
+    """Extra -D / -mllvm flags of a tuning experiment (FPA_HIPCC_FLAGS), empty for a normal build."""
+    return os.environ.get("FPA_HIPCC_FLAGS", "").split()
+
+
+def _baked_hash():
+    """The hash baked into the library: the source hash, plus a digest of FPA_HIPCC_FLAGS when they are
+    set, so that the loader refuses such a library unless told to accept it (FPA_ALLOW_TUNING_BUILD)."""
+    h, extra = _srchash(), _extra_flags()
+    if extra:
+        import hashlib
+        h += "+" + hashlib.sha256(" ".join(extra).encode()).hexdigest()[:8]
+    return h
+
+
 def _compile(src, defs=()):
     obj = os.path.join(BUILD, os.path.basename(src).replace(".hip", ".o"))
-    extra = os.environ.get("FPA_HIPCC_FLAGS", "").split()  # tuning experiments: extra -D / -mllvm flags
+    extra = _extra_flags()
     cmd = [hipcc()] + COMMON + list(defs) + PER_FILE.get(os.path.basename(src), []) + extra + ["-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -64,7 +79,7 @@ def build(verbose=True):
     srcs = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
     workers = min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
     # The source hash goes into fpa_api.hip only (fpa_source_hash()); the loader compares it.
-    defs = {s: ([f'-DFPA_SOURCE_HASH="{_srchash()}"'] if os.path.basename(s) == "fpa_api.hip" else [])
+    defs = {s: ([f'-DFPA_SOURCE_HASH="{_baked_hash()}"'] if os.path.basename(s) == "fpa_api.hip" else [])
             for s in srcs}
     with concurrent.futures.ThreadPoolExecutor(workers) as ex:
         objs = list(ex.map(lambda s: _compile(s, defs[s]), srcs))

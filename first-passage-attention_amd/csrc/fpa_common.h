@@ -240,53 +240,61 @@ __device__ __forceinline__ f32x16 mma_p2_p3(f32x16 acc, const f32x16 (&c)[NT], c
 // the block's 64 values in LDS (16-byte aligned): every read is unconditional (the same
 // address in all lanes) and positions past tr are masked by a select, so the scan has no
 // branches.  ALL_BEFORE: every key of the half is before every query of the wave (tr >= 32 * mt +
-// 32), no mask.
+// 32), no mask.  The values are read four at a time as the scan reaches them and each register
+// takes its value when the scan passes its key (the key of register j is 32*mt + k - 1 with
+// k = 8*(j/4) + 4*g + j%4 + 1: lane group 1 takes it at step k, lane group 0 four steps later), so
+// few registers are live at once.
 template <bool ALL_BEFORE = false>
 __device__ __forceinline__ void diag_x_keys(float (&X)[16], float &r, const float *phi, int mt, int tr, int g) {
-    float pv[33];
+    const bool g1 = g != 0;
+    const float top = (mt == 0) ? phi[32] : pinf();
+    // steps k = 32 .. 1 visit u = 32*mt + k; the value of step 32 is `top`
+    {
+        const int u = 32 * mt + 32;
+        r = fminf(r, (ALL_BEFORE || u <= tr) ? top : pinf());
+    }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 7; i >= 0; --i) {
         const f32x4 v = *reinterpret_cast<const f32x4 *>(phi + 32 * mt + 4 * i);
-        pv[4 * i] = v[0]; pv[4 * i + 1] = v[1]; pv[4 * i + 2] = v[2]; pv[4 * i + 3] = v[3];
-    }
-    pv[32] = (mt == 0) ? phi[32] : pinf();
-    float rr[33];
 #pragma unroll
-    for (int k = 32; k >= 1; --k) {
-        const int u = 32 * mt + k;
-        r = fminf(r, (ALL_BEFORE || u <= tr) ? pv[k] : pinf());
-        rr[k] = r;  // min phi[u .. tr]: the value for key u - 1
-    }
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const int k0 = 8 * (j / 4) + (j % 4);
-        X[j] = g ? rr[k0 + 5] : rr[k0 + 1];
+        for (int e = 3; e >= 0; --e) {
+            const int k = 4 * i + e;  // steps 31 .. 0 (step k + 1 was the previous one)
+            // after step k + 1 the running minimum is min phi[32*mt + k + 1 .. tr]: the value of the
+            // key 32*mt + k, i.e. of the register with 8*(j/4) + 4*g + j%4 = k
+            const int jj = 4 * (k / 8) + (k % 4);
+            if ((k % 8) >= 4)
+                X[jj] = r;  // lane group 1 (k = 8*(j/4) + 4 + j%4); group 0 overwrites it below
+            else
+                X[jj] = g1 ? X[jj] : r;  // lane group 0 (k = 8*(j/4) + j%4)
+            if (k >= 1) {
+                const int u = 32 * mt + k;
+                r = fminf(r, (ALL_BEFORE || u <= tr) ? v[e] : pinf());
+            }
+        }
     }
 }
 
 // Lane = key sr (0..63 in the block); registers = queries 32*mt + acc_row(j, g).  Ascending
 // scan; `r` carries min phi[sr+1 .. 32*mt - 1] in and min phi[sr+1 .. 32*mt + 31] out.
-// Branch-free like diag_x_keys.  ALL_AFTER: every query of the half is after every key of the
-// wave (sr < 32 * mt), no mask.
+// Branch-free like diag_x_keys, with the values read four at a time as the scan reaches them.
+// ALL_AFTER: every query of the half is after every key of the wave (sr < 32 * mt), no mask.
 template <bool ALL_AFTER = false>
 __device__ __forceinline__ void diag_x_queries(float (&X)[16], float &r, const float *phi, int mt, int sr, int g) {
-    float pv[32];
+    const bool g1 = g != 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const f32x4 v = *reinterpret_cast<const f32x4 *>(phi + 32 * mt + 4 * i);
-        pv[4 * i] = v[0]; pv[4 * i + 1] = v[1]; pv[4 * i + 2] = v[2]; pv[4 * i + 3] = v[3];
-    }
-    float rr[32];
 #pragma unroll
-    for (int k = 0; k < 32; ++k) {
-        const int u = 32 * mt + k;
-        r = fminf(r, (ALL_AFTER || u > sr) ? pv[k] : pinf());
-        rr[k] = r;  // min phi[sr+1 .. u]: the value for query u
-    }
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const int k0 = 8 * (j / 4) + (j % 4);
-        X[j] = g ? rr[k0 + 4] : rr[k0];
+        for (int e = 0; e < 4; ++e) {
+            const int k = 4 * i + e;
+            const int u = 32 * mt + k;
+            r = fminf(r, (ALL_AFTER || u > sr) ? v[e] : pinf());  // min phi[sr+1 .. u]: the value for query u
+            const int jj = 4 * (k / 8) + (k % 4);
+            if ((k % 8) < 4)
+                X[jj] = r;  // lane group 0 (query 8*(j/4) + j%4)
+            else
+                X[jj] = g1 ? r : X[jj];  // lane group 1 (query 8*(j/4) + 4 + j%4)
+        }
     }
 }
 
@@ -514,13 +522,28 @@ inline dim3 head_grid(int n, int H, int BH) { return dim3(n, H, BH / H); }
 // the dispatch order is rank-major over all heads (every head's heaviest tile first), so that the
 // longest tiles never wait for a free slot behind the short tiles of earlier heads.  The entry
 // points keep ntiles * BH below 2^31.
-__device__ __forceinline__ void xcd_work_item(int &rank, int &bh, int BH, int H, int ntiles) {
-    const int L = group_x() + ntiles * group_bh(H);
+//
+// slots > 1 (the workgroups one CU holds at once): the first round of dispatch places workgroup
+// k of a domain of ncu CUs (an XCD when heads are pinned, else the chip) on CU k % ncu, so a CU
+// starts with the workgroups k, k + ncu, k + 2 ncu, ...; when every workgroup is resident at once
+// (the launch is one round), the CU with the heaviest first-slot tile would otherwise also get the
+// heaviest tiles of the later slots and set the launch time.  Odd slots of the first round take
+// their tiles in reverse order instead (heavy + light + medium on every CU).
+__device__ __forceinline__ int snake_index(int k, int n, int ncu, int slots) {
+    const int s = k / ncu, c = k - s * ncu;
+    return ((s & 1) && s < slots && (s + 1) * ncu <= n) ? s * ncu + (ncu - 1 - c) : k;
+}
+constexpr int XCD_CUS = 32;  // CUs per XCD of MI355X (8 XCDs, 256 CUs)
+
+__device__ __forceinline__ void xcd_work_item(int &rank, int &bh, int BH, int H, int ntiles, int slots = 1) {
+    int L = group_x() + ntiles * group_bh(H);
     if ((BH & 7) == 0) {
-        const int xcd = L & 7, k = L >> 3, hpx = BH >> 3;
+        const int xcd = L & 7, hpx = BH >> 3;
+        const int k = slots > 1 ? snake_index(L >> 3, ntiles * hpx, XCD_CUS, slots) : (L >> 3);
         rank = k / hpx;
         bh = (k % hpx) * 8 + xcd;
     } else {
+        if (slots > 1) L = snake_index(L, ntiles * BH, 8 * XCD_CUS, slots);
         rank = L / BH;
         bh = L % BH;
     }

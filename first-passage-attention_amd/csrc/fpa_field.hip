@@ -374,11 +374,12 @@ __global__ void __launch_bounds__(256) fpa_field_scan_kernel(FieldParams p) {
     const float *gl = dl + (int64_t)p.H * p.TL, *hl = gl + (int64_t)p.H * p.TL;
     float *phi = p.phi + (int64_t)bh * p.T, *psi = p.psi + (int64_t)bh * p.T;
     float carry = 0.f;
-    for (int c0 = 0; c0 < p.T; c0 += 256 * SCK) {
+    // 64-bit positions: T may come within a chunk of 2^31 (check_field bounds B * TL below 2^31).
+    for (int64_t c0 = 0; c0 < p.T; c0 += 256 * SCK) {
         float d[SCK], g[SCK], e[SCK];
 #pragma unroll
         for (int k = 0; k < SCK; ++k) {
-            const int t = c0 + 256 * k + tid;
+            const int64_t t = c0 + 256 * k + tid;
             const bool ok = t < p.T;
             d[k] = ok ? dl[t] : 0.f;
             g[k] = ok ? gl[t] : 0.f;
@@ -386,7 +387,7 @@ __global__ void __launch_bounds__(256) fpa_field_scan_kernel(FieldParams p) {
         }
 #pragma unroll
         for (int k = 0; k < SCK; ++k) {
-            const int t = c0 + 256 * k + tid;
+            const int64_t t = c0 + 256 * k + tid;
             float total;
             const float run = carry + block_scan256(d[k], red, total);
             if (t < p.T) {
@@ -410,17 +411,17 @@ __global__ void __launch_bounds__(256) fpa_field_bwd_scan_kernel(FieldParams p) 
     float *dd = p.lin + ((int64_t)b * p.NO + h) * p.TL;
     float *dg = dd + (int64_t)p.H * p.TL, *dh = dg + (int64_t)p.H * p.TL;
     float carry = 0.f;
-    for (int c0 = 0; c0 < p.T; c0 += 256 * SCK) {
+    for (int64_t c0 = 0; c0 < p.T; c0 += 256 * SCK) {
         float a[SCK], c[SCK];
 #pragma unroll
         for (int k = 0; k < SCK; ++k) {
-            const int t = p.T - 1 - c0 - 256 * k - tid;
+            const int64_t t = p.T - 1 - c0 - 256 * k - tid;
             a[k] = t >= 0 ? dphi[t] : 0.f;
             c[k] = t >= 0 ? dpsi[t] : 0.f;
         }
 #pragma unroll
         for (int k = 0; k < SCK; ++k) {
-            const int t = p.T - 1 - c0 - 256 * k - tid;
+            const int64_t t = p.T - 1 - c0 - 256 * k - tid;
             float total;
             const float run = carry + block_scan256(a[k] + c[k], red, total);
             if (t >= 0) {
@@ -431,7 +432,8 @@ __global__ void __launch_bounds__(256) fpa_field_bwd_scan_kernel(FieldParams p) 
             carry += total;
         }
     }
-    if (p.T + tid < p.TL) dd[p.T + tid] = dg[p.T + tid] = dh[p.T + tid] = 0.f;
+    const int64_t tz = (int64_t)p.T + tid;
+    if (tz < p.TL) dd[tz] = dg[tz] = dh[tz] = 0.f;
 }
 
 // dx[b][t][c] = sum_o d(lin)[b][o][t] W[o][c] on the MFMA.  Grid (ceil(T / 64), B), NWF waves: the

@@ -23,6 +23,11 @@
 #ifndef FPA_FWD_WPE32
 #define FPA_FWD_WPE32 2
 #endif
+// Balance the tiles of the workgroups that share a CU in the first round of dispatch
+// (xcd_work_item); 0 keeps the heaviest-first order.
+#ifndef FPA_FWD_SNAKE
+#define FPA_FWD_SNAKE 1
+#endif
 
 namespace fpa {
 
@@ -130,7 +135,7 @@ fpa_fwd_kernel(FwdParams p) {
     const int w = __builtin_amdgcn_readfirstlane(tid / 64);  // wave index, uniform across the wave
     const int nqt = (p.T + BM - 1) / BM;
     int rank, bh;
-    xcd_work_item(rank, bh, p.BH, p.H, nqt);
+    xcd_work_item(rank, bh, p.BH, p.H, nqt, FPA_FWD_SNAKE ? WPE : 1);
     const int qt = nqt - 1 - rank;  // longest rows first
     const int b = bh / p.H, h = bh % p.H;
     const int q0 = qt * BM, qw0 = q0 + 32 * w, tq = qw0 + c;

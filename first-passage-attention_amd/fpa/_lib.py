@@ -6,6 +6,7 @@ library raises, so ``impl="hip"`` can never run on anything but the HIP kernels.
 """
 import ctypes
 import os
+import warnings
 
 import torch
 
@@ -105,8 +106,12 @@ def lib():
     L.fpa_source_hash.restype = ctypes.c_char_p
     built, here = L.fpa_source_hash().decode(), source_hash()
     if here is not None and built != here:
-        raise RuntimeError(f"libfpa.so was built from other sources (hash {built}, sources {here}): rebuild it "
-                           "with first-passage-attention_amd/build.py")
+        tuned = built.startswith(here + "+")  # these sources, built with extra FPA_HIPCC_FLAGS
+        if not (tuned and os.environ.get("FPA_ALLOW_TUNING_BUILD") == "1"):
+            why = ("was built with extra FPA_HIPCC_FLAGS (a tuning build; set FPA_ALLOW_TUNING_BUILD=1 to use it)"
+                   if tuned else f"was built from other sources (hash {built}, sources {here})")
+            raise RuntimeError(f"libfpa.so {why}: rebuild it with first-passage-attention_amd/build.py")
+        warnings.warn(f"libfpa.so is a tuning build ({built}): FPA_HIPCC_FLAGS were set when it was built")
     _LIB = L
     return L
 

@@ -241,6 +241,25 @@ def test_field_c_abi_validation(field, value, code, msg):
     assert msg in L.fpa_last_error().decode()
 
 
+@pytest.mark.parametrize("B,T,ok", [
+    (1, 2**31 - 16, True),     # T rounded up to 16 is 2^31 - 16: taken (then stopped by the NULL x)
+    (1, 2**31 - 15, False),    # rounds up to 2^31: refused before any launch
+    (2, 2**30 - 8, False),     # B * TL = 2^31
+    (2, 2**30 - 16, True),
+])
+def test_field_c_abi_length_bound(B, T, ok):
+    """B * TL (T rounded up to 16) must stay below 2^31, the bound the Field kernels' position
+    arithmetic is written for (their scans step in 64-bit positions, so the last chunk of a length
+    near 2^31 does not wrap); no GPU needed: refused or stopped before any launch."""
+    L = _lib.lib()
+    rc = L.fpa_field_fwd(_field_args(B=B, T=T, x=None), None)
+    err = L.fpa_last_error().decode()
+    if ok:
+        assert rc == _lib.FPA_ERR_INVALID and "non-NULL" in err, (rc, err)
+    else:
+        assert rc == _lib.FPA_ERR_UNSUPPORTED and "too large" in err, (rc, err)
+
+
 def test_field_workspace_size():
     """The projection as B*3H rows of T rounded up to 16 floats, plus the dW / dbias partials (at most
     64 splits of the positions)."""
@@ -259,6 +278,25 @@ def test_library_is_built_from_these_sources():
     L = _lib.lib()
     assert L.fpa_source_hash().decode() == source_hash()
     assert len(source_hash()) == 16
+
+
+def test_tuning_flags_change_the_baked_hash(monkeypatch):
+    """A library built with extra FPA_HIPCC_FLAGS carries the source hash plus a digest of the flags,
+    so the loader refuses it unless FPA_ALLOW_TUNING_BUILD=1 (no tuning build passes for a normal one)."""
+    import importlib.util
+    import os
+    from fpa._srchash import source_hash
+    spec = importlib.util.spec_from_file_location(
+        "fpa_build_t", os.path.join(os.path.dirname(_lib.__file__), "..", "build.py"))
+    b = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(b)
+    monkeypatch.delenv("FPA_HIPCC_FLAGS", raising=False)
+    assert b._baked_hash() == source_hash()
+    monkeypatch.setenv("FPA_HIPCC_FLAGS", "-DFPA_KV_CLASSES=0")
+    tuned = b._baked_hash()
+    assert tuned.startswith(source_hash() + "+") and len(tuned) == 16 + 1 + 8
+    monkeypatch.setenv("FPA_HIPCC_FLAGS", "-DFPA_KV_CLASSES=1")
+    assert b._baked_hash() != tuned
 
 
 def test_field_impl_is_validated():

@@ -56,8 +56,18 @@ def _case(hip, x, H, seed):
     (2, 300, 96, 12, torch.float16),
     (1, 64, 768, 32, torch.float32),
     (2, 45, 70, 3, torch.float16),     # C not a multiple of 4: the one-element-per-lane kernels in fp16
-    (2, 33, 20, 6, torch.float32),     # C = 20: a last projection step of 4 features
-    (3, 50, 36, 2, torch.float32),     # C = 36: waves with 16, 16 and 4 features
+    # Four-feature-aligned x, by output count NO = 3H: the staged projection takes NO <= 48 (tiles 1-3),
+    # proj16 NO > 48 (NT = 4 up to 64 outputs, NT = 6 beyond); the merged dx + dW launch has one
+    # instantiation per output range (<3,1> NO <= 12, <6,1> <= 16, <6,2> <= 24, <9,2> <= 32, <9,3> <= 36,
+    # <12,3> <= 48, <24,4> <= 64, <24,6> beyond).
+    (2, 33, 20, 6, torch.float32),     # staged (NO 18): chunk of 20 features, waves with 16 and 4; dxdw <6,2>
+    (3, 50, 36, 2, torch.float32),     # staged (NO 6): waves with 16, 16 and 4 features; dxdw <3,1>
+    (1, 60, 40, 5, torch.float32),     # staged (NO 15); dxdw <6,1>
+    (2, 50, 44, 9, torch.float16),     # staged (NO 27), fp16, C % 16 = 12; dxdw <9,2>
+    (2, 77, 88, 14, torch.float32),    # staged (NO 42), C % 16 = 8; dxdw <12,3>
+    (2, 70, 100, 20, torch.float32),   # proj16 NT = 4 (NO 60), last step of 4 features; dxdw <24,4>
+    (1, 90, 52, 17, torch.float16),    # proj16 NT = 4 (NO 51), fp16, last step of 4 features; dxdw <24,4>
+    (1, 40, 72, 24, torch.float32),    # proj16 NT = 6 (NO 72), last step of 8 features; dxdw <24,6>
     (1, 200, 768, 32, torch.float16),  # 96 outputs: six 16-wide tiles in fp16
 ])
 def test_field_matches_the_definition(hip, B, T, C, H, dtype):
@@ -71,12 +81,13 @@ def test_field_matches_the_definition(hip, B, T, C, H, dtype):
         assert _rel(a, r) <= tol, (name, _rel(a, r))
 
 
-@pytest.mark.parametrize("C", [64, 70])
-def test_field_without_dx(hip, C):
+@pytest.mark.parametrize("C,H", [(64, 4), (70, 4), (64, 8), (100, 20)])
+def test_field_without_dx(hip, C, H):
     """x that needs no gradient: the backward skips dx (a NULL dx in the C ABI) and still gives dW
-    and dbias, for aligned (C = 64) and unaligned (C = 70) features."""
-    _say(f"[field] no dx, C={C}")
-    B, T, H = 2, 90, 4
+    and dbias, for aligned (C = 64, 100: the dW kernel with 1, 2 and 4 output tiles) and unaligned
+    (C = 70) features."""
+    _say(f"[field] no dx, C={C} H={H}")
+    B, T = 2, 90
     g = torch.Generator().manual_seed(C)
     x = torch.randn(B, T, C, generator=g)
     w = torch.randn(3 * H, C, generator=g) / C ** 0.5

@@ -43,8 +43,8 @@ def run_hip(fpa, q, k, v, phi, psi, beta, do, tau=1.0):
     return [o.detach().cpu()] + [g.detach().cpu() for g in grads]
 
 
-def check(kern, ref, dtype):
-    for name, x, r in zip(NAMES, kern, ref):
+def check(kern, ref, dtype, names=NAMES):
+    for name, x, r in zip(names, kern, ref):
         want_dtype = dtype if name in ("o", "dq", "dk", "dv") else torch.float32
         assert x.dtype == want_dtype, (name, x.dtype)
         assert torch.isfinite(x).all(), name
@@ -157,19 +157,23 @@ def test_signed_beta_many_blocks(fpa, drift):
 def test_fp32_large_logits(fpa):
     """fp32 with beta < 0 over a long phi walk: the bias is positive and the logits reach several hundred
     (base 2).  The backward forms P from the forward's running maximum and log2 sum, so its P is the
-    forward's to a few ulps: dv (P^T dO) is held to 1e-5, the other gradients except dbeta to the fp32
-    bound.  dbeta is a sum of dS x over rows of dS that sum to zero (sum |dS x| / |dbeta| is about 1e4
-    here), and the fp32 rounding of the stored output alone moves it by about 1e-2 relative, in any
-    backward that takes Delta from that output; it is only checked for finiteness."""
+    forward's to a few ulps: dv (P^T dO) is held to 1e-5, every other gradient to the fp32 bound.
+    dbeta, a sum of dS x over rows of dS that sum to zero, is also held to the oracle fed the kernel's
+    own stored output (``fpa_grads_stored``: Delta taken from that output, everything else exact), the
+    quantity the reference's backward computes (kernel.py:165-174); measured 9e-6 against the exact
+    oracle and 4e-5 against the stored-output one."""
     _say("[parity] fp32 beta < 0, T=1531 D64, phi scale 4")
     q, k, v, phi, psi, _, do = O.make_inputs(1, 2, 1531, 64, dtype=torch.float32, seed=2005, phi_scale=4.0,
                                              psi_noise=0.1)
     beta = torch.tensor([-0.9, -1.3])
     kern = run_hip(fpa, q, k, v, phi, psi, beta, do, tau=0.5)
     ref = O.fpa_grads(q, k, v, phi, psi, beta, do, tau=0.5)
-    check(kern[:6], ref[:6], torch.float32)
+    check(kern, ref, torch.float32)
     assert O.rel_err(kern[3], ref[3]) <= 1e-5, ("dv", O.rel_err(kern[3], ref[3]))
-    assert torch.isfinite(kern[6]).all()
+    stored = O.fpa_grads_stored(q, k, v, phi, psi, beta, do, tau=0.5, store=torch.float32, o_stored=kern[0])
+    err = O.rel_err(kern[6], stored[6])
+    _say(f"[parity] fp32 large logits: dbeta vs stored-output oracle {err:.2e}, vs exact {O.rel_err(kern[6], ref[6]):.2e}")
+    assert err <= TOL[torch.float32], ("dbeta", err)
 
 
 def test_scalar_beta_and_strided_views(fpa):
@@ -293,24 +297,26 @@ def test_cfg4_shape_prefix(fpa):
 
 def test_large_scores(fpa):
     """q and k scaled by 60 in fp16: row maxima of q.k reach 1.4e5, far outside the usual range,
-    which stresses how -lse and -Delta enter the score accumulators.  In this regime dphi and
-    dbeta are ill-conditioned: the fp16 rounding of o, from which Delta is taken as in the
-    reference, alone moves dphi by 1.7e-2 and dpsi by 5e-4 relative to the float64 oracle
-    (measured with the oracle's float64 arithmetic and o rounded to fp16), and fp32 rounding of
-    scores near 1e5 moves P by ~1e-3.  Bounds: 1e-2 for o, dq, dk, dv, dpsi; 1e-1 for dphi and
-    dbeta (two accumulation orders that are both exact to fp32 rounding measured 3.0e-2 and
-    5.2e-2 there); everything finite."""
+    which stresses how -lse and -Delta enter the score accumulators.  o is held to the exact oracle
+    and every gradient to the oracle fed the kernel's own stored output (Delta taken from the fp16
+    output, as the reference's _bwd_delta does, kernel.py:165-174; against the exact gradients that
+    rounding alone moves dphi by 1.7e-2), at the fp16 bounds, except dphi.  The fp32 score
+    accumulators hold values near 1.4e5 (an ulp of 0.008), so each logit carries a rounding of a few
+    1e-3 (base 2) and P of a few 1e-3 relative, in any fp32 evaluation of these scores (the
+    reference's `tl.dot` accumulates in fp32 too); dphi, a soft-min-weighted sum of gated dS over
+    pairs whose rows cancel, takes that as 3.7e-3 and is held to 1e-2."""
     _say("[parity] B1 H2 T256 D64 fp16, q and k x60")
     q, k, v, phi, psi, beta, do = O.make_inputs(1, 2, 256, 64, dtype=torch.float16, seed=61)
     q, k = (q.float() * 60).half(), (k.float() * 60).half()
     kern = run_hip(fpa, q, k, v, phi, psi, beta, do)
-    ref = O.fpa_grads(q, k, v, phi, psi, beta, do)
+    exact = O.fpa_grads(q, k, v, phi, psi, beta, do)
+    stored = O.fpa_grads_stored(q, k, v, phi, psi, beta, do, o_stored=kern[0])
+    ref = [exact[0]] + stored[1:]
     errs = {name: O.rel_err(x, r) for name, x, r in zip(NAMES, kern, ref)}
-    _say("[parity] large-score errors " + " ".join(f"{n}={e:.2e}" for n, e in errs.items()))
-    for name, x in zip(NAMES, kern):
-        assert torch.isfinite(x).all(), name
-        tol = 1e-1 if name in ("dphi", "dbeta") else 1e-2
-        assert errs[name] <= tol, (name, errs[name])
+    _say("[parity] large-score errors (stored-output oracle) " + " ".join(f"{n}={e:.2e}" for n, e in errs.items()))
+    check([x for n, x in zip(NAMES, kern) if n != "dphi"], [r for n, r in zip(NAMES, ref) if n != "dphi"],
+          torch.float16, names=[n for n in NAMES if n != "dphi"])
+    assert torch.isfinite(kern[4]).all() and errs["dphi"] <= 1e-2, ("dphi", errs["dphi"])
 
 
 def test_graph_replay_matches_eager(fpa):

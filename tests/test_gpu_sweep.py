@@ -18,12 +18,13 @@ level of the backward's own fp32 arithmetic, against the exact gradients; o agai
 forward.
 
 The draws stay in the reference's data model (psi = phi + noise of at most 0.5, phi scale up to 4).
-The long draws (16 to 32 blocks) keep to beta > 0, the reference's domain (kernel.py:7).  With
-beta < 0 the bias is positive and grows with the range of the walk: at T = 1531 and phi scale 4
-the logits and lse reach 630 (base 2), where an fp32 exponent is good to 3e-5, and any evaluation
-that recomputes P from a stored fp32 lse (the reference's backward, kernel.py:216, as well as
-this one) moves dbeta, whose condition number sum |dS x| / |dbeta| is 2.5e4 there, by about 1e-2.
-Negative and mixed beta are drawn at the shorter lengths, where the bias stays small.
+With beta < 0 the bias is positive and grows with the range of the walk: at T = 1531 and phi scale 4
+the logits and lse reach 630 (base 2).  dbeta, a sum of dS x over rows of dS that cancel (its condition
+number sum |dS x| / |dbeta| reaches 2.5e4 there), can then move by up to 1e-2 from the fp32 rounding
+of the stored output alone (one such draw, B2 H3 D64, measured 9.5e-3), so in the long fp32 draws
+with negative or mixed beta dbeta is checked, like the fp16 gradients, against ``fpa_grads_stored``
+given the kernel's own output, at the fp32 bound; the backward forms P from the forward's running
+maximum and log2 sum, so the other gradients are held to the exact oracle.
 """
 import random
 import sys
@@ -62,12 +63,15 @@ def _cases(n=16, seed=2026, lengths=(1, 37, 64, 129, 200, 333, 512, 701), first=
 # every per-block class occurs), beta > 0; six draws at D = 256 (the single-wave-per-SIMD kernels); six
 # with phi rounded to integers (equal values inside ranges: tied minima and equal soft-min weights); four
 # long fp16 draws with beta of either sign; six at extreme temperatures (tau 0.1: the soft-min weights
-# near one-hot over spans of a few units of phi; tau 8: near-uniform).
+# near one-hot over spans of a few units of phi; tau 8: near-uniform); four long fp32 draws with
+# negative or mixed beta.
 CASES = (_cases() + _cases(n=6, seed=7, lengths=(1000, 1531, 2048), first=2000, betas=("positive",))
          + _cases(n=6, seed=11, lengths=(3, 65, 190, 449, 640), first=3000, dims=(256,))
          + _cases(n=6, seed=13, lengths=(97, 256, 511, 800), first=4000, ties=True)
          + _cases(n=4, seed=17, lengths=(1000, 1531, 2048), first=5000, betas=("negative", "mixed"), dtypes=("f16",))
-         + _cases(n=6, seed=19, lengths=(64, 300, 777), first=6000, betas=("positive", "mixed"), taus=(0.1, 8.0)))
+         + _cases(n=6, seed=19, lengths=(64, 300, 777), first=6000, betas=("positive", "mixed"), taus=(0.1, 8.0))
+         + _cases(n=4, seed=23, lengths=(1000, 1531, 2048), first=7000, betas=("negative", "mixed"), dtypes=("f32",),
+                  dims=(16, 32, 64)))
 
 
 def _say(*a):
@@ -106,7 +110,15 @@ def test_sweep_matches_the_oracle(fpa, case):
     kern = run_hip(fpa, q, k, v, phi, psi, beta, do, tau=c["tau"])
     exact = O.fpa_grads(q, k, v, phi, psi, beta, do, tau=c["tau"])
     if dtype == torch.float32:
-        check(kern, exact, dtype)
+        if c["T"] >= 1000 and c["beta"] in ("negative", "mixed"):
+            check(kern[:6], exact[:6], dtype)
+            stored = O.fpa_grads_stored(q, k, v, phi, psi, beta, do, tau=c["tau"], store=torch.float32,
+                                        o_stored=kern[0])
+            _say(f"[sweep] dbeta vs stored-output oracle {O.rel_err(kern[6], stored[6]):.2e}, "
+                 f"vs exact {O.rel_err(kern[6], exact[6]):.2e}")
+            assert torch.isfinite(kern[6]).all() and O.rel_err(kern[6], stored[6]) <= 2e-4, "dbeta"
+        else:
+            check(kern, exact, dtype)
         return
     check(kern[:1], exact[:1], dtype)
     ref = O.fpa_grads_stored(q, k, v, phi, psi, beta, do, tau=c["tau"], o_stored=kern[0])
