@@ -2,6 +2,7 @@
 """Benchmark of First Passage Attention on one MI355X (the BASELINE.json metric).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg2|cfg3|cfg4] [--no-extra] [--no-cpu]
+    python bench.py --shape B,H,T,D [--dtype fp16|fp32] [--rounds N] [--json FILE]   # any shape
     python bench.py --workload lm [--steps K] [--warmup W]     # the cfg5 LM training step alone
 
 A step is one forward + backward of ``first_passage_attention(..., impl="hip")`` over one batch of
@@ -17,6 +18,12 @@ The default run adds, under ``configs``, the other BASELINE.json workloads: cfg3
 forward+backward ms, % of the dtype's MFMA peak) and cfg5 (one training step of fpa.lm.FPADecoder: a
 12-layer d768 H12 pre-norm decoder over B8 x T2048 random tokens, fp16 autocast, gradient scaler,
 AdamW; tokens/s).
+
+``ref_protocol`` repeats the measurement with the reference bench's protocol (its bench.py:11-23,
+50-54): each call timed alone between two HIP events, 3 warm-ups + 15 timed calls, the median, over
+--rounds rounds (5), the median of the rounds; its fwd+bwd call clones the six inputs as the
+reference's does.  --shape / --dtype time any shape with that protocol and the step above (the
+config's distributions, dO = 1); --json also writes the line to a file.
 
 Per-kernel times come from HIP events recorded on torch's current stream (the stream every kernel is
 launched on) around C-ABI calls that enqueue one kernel each; the dominant kernel's duration gives
@@ -224,6 +231,60 @@ def time_steps(fn, steps, warmup):
     return (time.perf_counter() - t0) * 1e3 / steps
 
 
+def time_ref_protocol(fn, rounds, warm=3, n=15):
+    """The reference bench's timing (its bench.py:11-23, 50-54): per round, `warm` untimed calls, then `n`
+    calls each between two events on the current stream with a synchronisation after each, median; the
+    median over `rounds` rounds.  Returns (median ms, per-round ms)."""
+    import torch
+    per_round = []
+    for _ in range(rounds):
+        for _ in range(warm):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(n):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b))
+        per_round.append(statistics.median(ts))
+    return statistics.median(per_round), per_round
+
+
+def committed_counters(config, kernel):
+    """MfmaUtil and VALUBusy (%) of `kernel` from the committed counter summary
+    (profiles/fpa_<config>_counters.md), or None."""
+    path = os.path.join(ROOT, "profiles", f"fpa_{config}_counters.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 3 and cells[0].startswith(kernel):
+            try:
+                return {"mfma_util_pct": float(cells[1]), "valu_busy_pct": float(cells[2])}
+            except ValueError:
+                return None
+    return None
+
+
+def committed_kernel_us(config, kernel):
+    """Average duration (us) of `kernel` in the committed rocprofv3 kernel-trace summary
+    (profiles/fpa_<config>_kernel_trace.md), or None."""
+    path = os.path.join(ROOT, "profiles", f"fpa_{config}_kernel_trace.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 3 and cells[0].startswith(kernel):
+            try:
+                return float(cells[2])
+            except ValueError:
+                return None
+    return None
+
+
 def time_config(cfg, steps, warmup):
     """Forward and forward+backward ms of one config (inputs resident, leaves kept across steps)."""
     import torch
@@ -262,6 +323,10 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline legs")
     ap.add_argument("--no-extra", action="store_true", help="skip the other configs (cfg3, cfg4, cfg5)")
+    ap.add_argument("--shape", help="B,H,T,D: time this shape instead of --config (the config's distributions)")
+    ap.add_argument("--dtype", choices=("fp16", "fp32"), default=None, help="with --shape (default fp16)")
+    ap.add_argument("--rounds", type=int, default=5, help="rounds of the reference's timing protocol")
+    ap.add_argument("--json", help="also write the JSON line to this file")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="first run one device-to-device copy of this many MiB (a known-size kernel that "
                          "calibrates the FETCH_SIZE / WRITE_SIZE counters of a profiling run)")
@@ -280,7 +345,12 @@ def main():
     import fpa
     from fpa import _hip, _lib
 
-    cfg = CONFIGS[a.config]
+    cfg = dict(CONFIGS[a.config])
+    custom = a.shape is not None
+    if custom:
+        B, H, T, D = (int(x) for x in a.shape.split(","))
+        cfg.update(B=B, H=H, T=T, D=D, dtype="f32" if a.dtype == "fp32" else "f16")
+        a.no_extra = True
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if a.copy_mib:
@@ -323,6 +393,8 @@ def main():
             fpa.first_passage_attention(*inputs, impl="hip")
 
     fwd_ms = time_steps(fwd, a.steps, a.warmup)
+    ref_fwd, ref_fwd_rounds = time_ref_protocol(fwd, a.rounds)
+    ref_fb, ref_fb_rounds = time_ref_protocol(step_with_clones, a.rounds)
 
     # Per-kernel durations: one C-ABI call per kernel (phases), HIP events on the launch stream.
     qr, kr, vr = _hip.rows(q), _hip.rows(k), _hip.rows(v)
@@ -359,7 +431,6 @@ def main():
     dom = max(kernels, key=lambda n: kernels[n][0])
     dom_ms, dom_flops = kernels[dom]
     peak = PEAK_TFLOPS[cfg["dtype"]]
-    achieved = dom_flops / (dom_ms * 1e-3) / 1e12
 
     fwd_flops, fb_flops = 4 * D * P, 14 * D * P
     fb_tflops = fb_flops / (fwd_bwd_ms * 1e-3) / 1e12
@@ -397,8 +468,8 @@ def main():
         "vs_baseline": None,
         "dtype": cfg["dtype"],
         "data": "synthetic",
-        "config": {"workload": f"{a.config}: FPA forward+backward B{cfg['B']} H{cfg['H']} T{cfg['T']} "
-                               f"D{cfg['D']} {cfg['dtype']}, dO = 1 (loss o.float().sum())",
+        "config": {"workload": f"{'custom' if custom else a.config}: FPA forward+backward B{cfg['B']} H{cfg['H']} "
+                               f"T{cfg['T']} D{cfg['D']} {cfg['dtype']}, dO = 1 (loss o.float().sum())",
                    "B": cfg["B"], "H": cfg["H"], "T": cfg["T"], "D": D, "parallelism": "single GPU"},
         "fwd_ms": round(fwd_ms, 4),
         "fwd_bwd_ms": round(fwd_bwd_ms, 4),
@@ -407,17 +478,44 @@ def main():
         "fwd_tflops": round(fwd_tflops, 3),
         "fwd_pct_peak": round(100 * fwd_tflops / peak, 2),
         "fwd_bwd_pct_peak": round(100 * fb_tflops / peak, 2),
+        "ref_protocol": {"fwd_ms": round(ref_fwd, 4), "fwd_bwd_ms": round(ref_fb, 4),
+                         "fwd_bwd_pct_peak": round(100 * fb_flops / (ref_fb * 1e-3) / 1e12 / peak, 2),
+                         "rounds_ms": {"fwd": [round(x, 4) for x in ref_fwd_rounds],
+                                       "fwd_bwd": [round(x, 4) for x in ref_fb_rounds]},
+                         "protocol": f"median of {a.rounds} rounds x (3 warm-ups + median of 15 event-timed "
+                                     "calls, synchronised after each); fwd+bwd clones the inputs "
+                                     "(reference bench.py:11-23, 44-54)"},
         "kernel_ms": {n: round(t, 4) for n, (t, _) in kernels.items()},
-        "roofline": {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 3), "peak": peak,
-                     "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
-                     "traffic": measured_traffic(a.config, dom),
-                     "note": "priced against the dense MFMA peak of the dtype; the kernel's own limiter "
-                             "(VALU issue or MFMA) is in profiles/fpa_<config>_counters.md"},
+        "roofline": roofline(a.config, custom, dom, dom_ms, dom_flops, peak),
         "configs": extra,
         "cpu_baseline": cpu,
         "cpu_baseline_cfg1": cpu1,
     }
-    print(json.dumps(res), flush=True)
+    line = json.dumps(res)
+    print(line, flush=True)
+    if a.json:
+        with open(a.json, "w") as f:
+            f.write(line + "\n")
+
+
+def roofline(config, custom, dom, dom_ms, dom_flops, peak):
+    """The dominant kernel against the dense MFMA peak of the dtype.  `bound` is its roofline regime by
+    arithmetic intensity (10 D flops per pair against a few bytes: far above the ridge of 2.5e15 / 8e12
+    flop/B, so "mfma"); `limiter` is what the committed counters show issuing most (VALU or MFMA), and
+    `frac_profile` the same fraction from the committed rocprofv3 trace, measured on another box (MI355X
+    boxes differ by a few percent)."""
+    achieved = dom_flops / (dom_ms * 1e-3) / 1e12
+    r = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 3), "peak": peak, "unit": "TFLOP/s",
+         "frac": round(achieved / peak, 4), "traffic": None if custom else measured_traffic(config, dom)}
+    cnt = None if custom else committed_counters(config, dom)
+    if cnt:
+        r["limiter"] = dict(cnt, unit="VALU" if cnt["valu_busy_pct"] > cnt["mfma_util_pct"] else "MFMA",
+                            source=f"profiles/fpa_{config}_counters.md")
+    us = None if custom else committed_kernel_us(config, dom)
+    if us:
+        r["profile_us"] = us
+        r["frac_profile"] = round(dom_flops / (us * 1e-6) / 1e12 / peak, 4)
+    return r
 
 
 if __name__ == "__main__":
