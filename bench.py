@@ -9,7 +9,10 @@ A step is one forward + backward of ``first_passage_attention(..., impl="hip")``
 synthetic inputs already resident in HBM (BASELINE.json config 2 by default: B4 H12 T2048 D64 fp16;
 q,k,v ~ N(0,1); phi = cumsum N(0,1); psi = phi + N(0,1); beta = 1; the gradients of the config's loss
 o.float().sum(), i.e. dO = 1, w.r.t. q, k, v, phi, psi, beta).  W untimed steps, then K steps timed
-between two device synchronisations.  One JSON line.  ``value`` is fwd+bwd TFLOP/s of the algorithmic
+between two device synchronisations.  Before the W warm-up steps the step runs for ``--settle``
+seconds (0.3) untimed: MI355X needs some tens of milliseconds of load before its clocks settle, and a
+timed region of a few milliseconds right after start measures up to 15% slow (20 steps after 5
+warm-ups, cfg2: 0.275-0.279 ms; after 0.05 s of steps: 0.237 ms, the sum of the kernels).  One JSON line.  ``value`` is fwd+bwd TFLOP/s of the algorithmic
 flops 14*D*P (P = B*H*T*(T+1)/2 causal pairs; bias and soft-min work not counted).
 ``fwd_bwd_ms_with_clones`` times the reference bench's step (bench.py:46-48 of the reference: fresh
 clones of the six inputs, forward, backward) beside it.
@@ -218,6 +221,16 @@ def run_lm(a):
     print(json.dumps(res), flush=True)
 
 
+def settle(fn, seconds):
+    """Run fn untimed for about `seconds` of wall time (device clocks settle under load)."""
+    import torch
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+
+
 def time_steps(fn, steps, warmup):
     """ms per call of fn over `steps` back-to-back calls between two device synchronisations."""
     import torch
@@ -327,6 +340,8 @@ def main():
     ap.add_argument("--dtype", choices=("fp16", "fp32"), default=None, help="with --shape (default fp16)")
     ap.add_argument("--rounds", type=int, default=5, help="rounds of the reference's timing protocol")
     ap.add_argument("--json", help="also write the JSON line to this file")
+    ap.add_argument("--settle", type=float, default=0.3,
+                    help="seconds of untimed steps before the warm-up (device clocks settle under load)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="first run one device-to-device copy of this many MiB (a known-size kernel that "
                          "calibrates the FETCH_SIZE / WRITE_SIZE counters of a profiling run)")
@@ -371,6 +386,7 @@ def main():
         x = [t.clone().requires_grad_() for t in inputs]
         fpa.first_passage_attention(*x, impl="hip").backward(do)
 
+    settle(step, a.settle)
     fwd_bwd_ms = time_steps(step, a.steps, a.warmup)
     clones_ms = time_steps(step_with_clones, a.steps, a.warmup)
 
@@ -471,6 +487,7 @@ def main():
         "config": {"workload": f"{'custom' if custom else a.config}: FPA forward+backward B{cfg['B']} H{cfg['H']} "
                                f"T{cfg['T']} D{cfg['D']} {cfg['dtype']}, dO = 1 (loss o.float().sum())",
                    "B": cfg["B"], "H": cfg["H"], "T": cfg["T"], "D": D, "parallelism": "single GPU"},
+        "settle_s": a.settle,
         "fwd_ms": round(fwd_ms, 4),
         "fwd_bwd_ms": round(fwd_bwd_ms, 4),
         "fwd_bwd_ms_with_clones": round(clones_ms, 4),
