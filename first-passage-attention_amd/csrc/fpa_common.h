@@ -408,6 +408,13 @@ template <typename T, int D, int DT, int NR, int NW> struct TileLoader {
             off[j] = (uint32_t)((r * st + lc * P::CE) * (int64_t)sizeof(T));
         }
     }
+    // issue() for a tile whose rows are all below T: no per-lane clamping, so a loop that only loads
+    // such tiles keeps no clamped offsets live.
+    __device__ __forceinline__ void issue_full(uint32_t tile, const T *base, int64_t st, int row0, int wave) const {
+        const u32x4 rs = buf_rsrc(base + (int64_t)row0 * st);
+#pragma unroll
+        for (int j = 0; j < PER; ++j) buf_lds16(rs, off[j], tile + 1024 * min(wave + NW * j, NI - 1));
+    }
     // Rows row0 .. row0 + NR - 1 (wave-uniform row0 < T_) of the tensor whose row 0 is `base` into
     // `tile`, through a buffer resource based at row row0 (the offsets stay 32-bit).
     __device__ __forceinline__ void issue(uint32_t tile, const T *base, int64_t st, int row0, int T_, int wave,
