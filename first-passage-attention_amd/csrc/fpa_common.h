@@ -531,7 +531,7 @@ inline dim3 head_grid(int n, int H, int BH) { return dim3(n, H, BH / H); }
 // points keep ntiles * BH below 2^31.
 //
 // slots > 1 (the workgroups one CU holds at once): the first round of dispatch places workgroup
-// k of a domain of ncu CUs (an XCD when heads are pinned, else the chip) on CU k % ncu, so a CU
+// k of an XCD's ncu CUs (k counting that XCD's workgroups) on CU k % ncu, so a CU
 // starts with the workgroups k, k + ncu, k + 2 ncu, ...; when every workgroup is resident at once
 // (the launch is one round), the CU with the heaviest first-slot tile would otherwise also get the
 // heaviest tiles of the later slots and set the launch time.  Odd slots of the first round take
@@ -550,7 +550,9 @@ __device__ __forceinline__ void xcd_work_item(int &rank, int &bh, int BH, int H,
         rank = k / hpx;
         bh = (k % hpx) * 8 + xcd;
     } else {
-        if (slots > 1) L = snake_index(L, ntiles * BH, 8 * XCD_CUS, slots);
+        // Reversed within each XCD (L & 7 kept), so that an item stays on the XCD of the plain
+        // order and each XCD's L2 keeps seeing the same heads.
+        if (slots > 1) L = (snake_index(L >> 3, (ntiles * BH) >> 3, XCD_CUS, slots) << 3) | (L & 7);
         rank = L / BH;
         bh = L % BH;
     }
