@@ -87,7 +87,7 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
     extern __shared__ float dyn[];
     __shared__ float sA[G], sC[G], sc[G], sW[G], sR[G];
     __shared__ float segM[4][G], segZ[4][G], segM2[4][G], segZ2[4][G], segA[4][G], segB[4][G], pp[4][G];
-    __shared__ float contrib[G][G + 1];      // [u][s]
+    __shared__ float contrib[G][G + 1];      // [u][s]; before that, the block's gd tile as [s][t]
     __shared__ float sF[G], sH[G];           // single-reference key-block and query-block terms
     __shared__ float sE[G];                  // 2^{a_u - c_U} (0 past the block's last position)
     __shared__ float red[4];
@@ -103,15 +103,15 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
     const int NB = p.NB;
     float *sBM = dyn, *scanA = dyn + NB, *scanB = dyn + 2 * NB;
 
-    // This lane's 16 gated in-block dS values (column s = lane, rows u in [16w, 16w + 16)),
-    // loaded first so that their latency overlaps the setup below.  A column with no row u > s in
-    // this range (s >= 16w + 15) has no pair here: its values are never read and are not loaded.
-    f32x4 gq[4];
-    {
-        const f32x4 *gsrc = reinterpret_cast<const f32x4 *>(p.gd + ((brow + U) * G + lane) * G + 16 * w);
-        const bool need = lane < 16 * w + 15;
+    // The block's gated in-block dS tile (gd, [s][t], 16 KB), loaded first so that the latency overlaps
+    // the setup below: 16-byte pieces in order (each wave instruction reads 1 KB of contiguous memory),
+    // staged in `contrib` (pitch G + 1: the column reads below are free of bank conflicts) before the
+    // first barrier.  A piece with no pair s < t (every t <= s) is never read and is not loaded.
+    f32x4 gl[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) gq[i] = need ? gsrc[i] : f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < 4; ++i) {
+        const int q = tid + NTHREADS * i, s = q >> 4, t0 = 4 * (q & 15);
+        gl[i] = (t0 + 3 > s) ? reinterpret_cast<const f32x4 *>(p.gd + (brow + U) * G * G)[q] : f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
     if (U == 0 && b == 0) {  // dbeta[h] = sum over batches and key-side partials
@@ -145,7 +145,18 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
         }
     }
     for (int i = tid; i < NB; i += NTHREADS) sBM[i] = -p.state[L.bplane(BP_MIN) + brow + i] * il2;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int q = tid + NTHREADS * i, s = q >> 4, t0 = 4 * (q & 15);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) contrib[s][t0 + e] = gl[i][e];
+    }
     __syncthreads();
+    // This lane's 16 values: column s = lane, rows u in [16w, 16w + 16).  Read before any wave writes
+    // contrib again (after at least one more barrier).
+    float gq[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) gq[k] = contrib[lane][16 * w + k];
     const float cU = sBM[U];
     const int nI = NB - 1 - U;
     const int npairs = U * nI;
@@ -196,7 +207,7 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
             Z += ev[k];
-            qv[k] = (ev[k] > 0.f) ? gq[k / 4][k % 4] * frcp(Z) : 0.f;
+            qv[k] = (ev[k] > 0.f) ? gq[k] * frcp(Z) : 0.f;
             Qs += qv[k];
         }
         segA[w][s] = Qs;
@@ -266,7 +277,7 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
                 const float m1 = (k < 15) ? mv[k + 1] : mnext;
                 const float z1 = (k < 15) ? zv[k + 1] : znext;
                 rho[k] = (u < last) ? zv[k] * fexp2(mv[k] - m1) * frcp(z1) : 0.f;
-                gv[k] = gq[k / 4][k % 4];
+                gv[k] = gq[k];
                 lam = fmaf(rho[k], lam, gv[k]);
                 Bc *= rho[k];
             }
