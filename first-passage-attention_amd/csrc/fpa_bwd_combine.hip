@@ -169,10 +169,18 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
         // cmid(ib, jb) = max(A_jb, c_U, B_ib), A_jb = max over (jb, U) = scanA[jb + 1],
         // B_ib = max over (U, ib) = scanB[ib - 1].  Consecutive threads read consecutive jb.
         float acc = 0.f;
+        // Pair idx = (ib - U - 1) * U + jb, stepped by NTHREADS without a division per step.
+        const int dq = NTHREADS / U, dr = NTHREADS - dq * U;
+        int ib = U + 1 + tid / U, jb = tid % U;
         for (int idx = tid; idx < npairs; idx += NTHREADS) {
-            const int ib = U + 1 + idx / U, jb = idx % U;
             const float cm = fmaxf(fmaxf(scanA[jb + 1], cU), scanB[ib - 1]);
             acc += fexp2(cU - cm) * p.tbuf[(brow + ib) * NB + jb];
+            jb += dr;
+            ib += dq;
+            if (jb >= U) {
+                jb -= U;
+                ++ib;
+            }
         }
         SU = block_sum_256(acc, red, w, lane);
     }
