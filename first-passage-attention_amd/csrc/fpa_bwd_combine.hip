@@ -169,17 +169,39 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
         // cmid(ib, jb) = max(A_jb, c_U, B_ib), A_jb = max over (jb, U) = scanA[jb + 1],
         // B_ib = max over (U, ib) = scanB[ib - 1].  Consecutive threads read consecutive jb.
         float acc = 0.f;
-        // Pair idx = (ib - U - 1) * U + jb, stepped by NTHREADS without a division per step.
-        const int dq = NTHREADS / U, dr = NTHREADS - dq * U;
-        int ib = U + 1 + tid / U, jb = tid % U;
-        for (int idx = tid; idx < npairs; idx += NTHREADS) {
-            const float cm = fmaxf(fmaxf(scanA[jb + 1], cU), scanB[ib - 1]);
-            acc += fexp2(cU - cm) * p.tbuf[(brow + ib) * NB + jb];
-            jb += dr;
-            ib += dq;
-            if (jb >= U) {
-                jb -= U;
-                ++ib;
+        if (npairs <= NTHREADS) {  // uniform: one pair per thread at most
+            if (tid < npairs) {
+                const int ib = U + 1 + tid / U, jb = tid % U;
+                const float cm = fmaxf(fmaxf(scanA[jb + 1], cU), scanB[ib - 1]);
+                acc = fexp2(cU - cm) * p.tbuf[(brow + ib) * NB + jb];
+            }
+        } else {
+            // Pair idx = (ib - U - 1) * U + jb, stepped by NTHREADS without a division per step; four
+            // steps' loads are issued before their terms are added (in the order of idx).
+            const int dq = NTHREADS / U, dr = NTHREADS - dq * U;
+            int ib = U + 1 + tid / U, jb = tid % U;
+            constexpr int UNR = 4;
+            for (int idx = tid; idx < npairs; idx += UNR * NTHREADS) {
+                float tv[UNR];
+                int ibv[UNR], jbv[UNR];
+#pragma unroll
+                for (int r = 0; r < UNR; ++r) {
+                    const bool ok = idx + r * NTHREADS < npairs;
+                    ibv[r] = ok ? ib : U + 1;  // in range for the scans below; the term is 0
+                    jbv[r] = ok ? jb : 0;
+                    tv[r] = ok ? p.tbuf[(brow + ib) * NB + jb] : 0.f;
+                    jb += dr;
+                    ib += dq;
+                    if (jb >= U) {
+                        jb -= U;
+                        ++ib;
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < UNR; ++r) {
+                    const float cm = fmaxf(fmaxf(scanA[jbv[r] + 1], cU), scanB[ibv[r] - 1]);
+                    acc += fexp2(cU - cm) * tv[r];
+                }
             }
         }
         SU = block_sum_256(acc, red, w, lane);
