@@ -82,6 +82,81 @@ __device__ __forceinline__ float block_sum_256(float x, float *red, int w, int l
     return r;
 }
 
+// From this many blocks per head on, the middle-block sums run in O(NB^2) per head: the mid kernel
+// below turns each row of TBUF into prefix sums first, and the combine reads one sum per query block.
+// Below it the combine sums every (query block, key block) pair around each block, O(NB^3 / 6) per
+// head, which costs less than a second launch.
+constexpr int MID_SCAN_NB = 128;
+
+// Row i (query block) of a head's TBUF holds V(i, j) = 2^{cmid(i, j)} M(i, j) for key blocks j <= i - 2,
+// M(i, j) the middle-block soft-min sum of the block pair and cmid(i, j) = max a over blocks j+1 .. i-1.
+// The middle-block part of dphi in block U needs S_U = sum_{j < U < i} M(i, j).  With
+// m_U = max a over blocks U .. i-1 (c_b = max a over block b), the row's prefix sums
+//   Q_i(U) = 2^{m_U} sum_{j < U} M(i, j),   U = 1 .. i - 1,
+// follow Q_i(U + 1) = 2^{m_{U+1} - m_U} Q_i(U) + V(i, U) from Q_i(0) = 0, every factor at most 1, and
+// S_U = sum_{i > U} 2^{-m_U} Q_i(U).  One wave per row: each lane takes a segment of U, composes the
+// segment's affine map (going down, with m_U as a running maximum), the maps are scanned across the
+// lanes, and each lane reruns its segment upward from the value entering it.  Q_i(U) goes to the
+// upper triangle of the head's TBUF matrix (row U, column i > U), which the key side never writes;
+// its m_U values are parked there between the two passes.
+__global__ void __launch_bounds__(NTHREADS) fpa_bwd_mid_kernel(BwdParams p) {
+    __shared__ float cb[MAX_NB];  // c_b for the head's blocks
+    const int bh = group_bh(p.H), tid = thread_x(), lane = tid % 64;
+    const int w = __builtin_amdgcn_readfirstlane(tid / 64);
+    const int NB = p.NB;
+    const int64_t brow = (int64_t)bh * NB;
+    const StateLayout L{p.BH, p.TP, p.NB};
+    const int i = __builtin_amdgcn_readfirstlane(group_x() * (NTHREADS / 64) + w);  // this wave's row
+    for (int b = tid; b < NB; b += NTHREADS) cb[b] = -p.state[L.bplane(BP_MIN) + brow + b] * p.il2;
+    __syncthreads();
+    if (i < 2 || i >= NB) return;  // wave-uniform: rows 0 and 1 have no pair
+    const float *V = p.tbuf + (brow + i) * NB;  // V(i, U) = V[U], U <= i - 2
+    float *col = p.tbuf + brow * NB + i;        // Q_i(U) = col[U * NB]
+    const int n = i - 1;                        // steps U = 0 .. n - 1
+    const int k = (n + 63) / 64, lo = min(lane * k, n), hi = min(lo + k, n);
+    // m_hi = max(c_hi .. c_{i-1}): the maxima of the later lanes' segments and c_{i-1}.
+    float smax = ninf();
+    for (int U = lo; U < hi; ++U) smax = fmaxf(smax, cb[U]);
+    float x = smax;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float y = __shfl_down(x, o, 64);
+        if (lane + o < 64) x = fmaxf(x, y);
+    }
+    float mhi = __shfl_down(x, 1, 64);
+    if (lane == 63) mhi = ninf();
+    mhi = fmaxf(mhi, cb[i - 1]);
+    // Pass 1, down the segment: the composed map Q(hi) = A Q(lo) + B; m_U parked for lo < U < hi.
+    float A = 1.f, B = 0.f, mnext = mhi;
+    for (int U = hi - 1; U >= lo; --U) {
+        const float m = fmaxf(cb[U], mnext);
+        B = fmaf(V[U], A, B);
+        A *= fexp2(mnext - m);
+        if (U > lo) col[(int64_t)U * NB] = m;
+        mnext = m;
+    }
+    const float mlo = mnext;
+    // Inclusive scan of the maps over the lanes (lane 0 first), then the value entering each segment.
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float Ap = __shfl_up(A, o, 64), Bp = __shfl_up(B, o, 64);
+        if (lane >= o) {
+            B = fmaf(A, Bp, B);
+            A *= Ap;
+        }
+    }
+    float q = __shfl_up(B, 1, 64);
+    if (lane == 0) q = 0.f;
+    // Pass 2, up the segment: Q(U + 1) = 2^{m_{U+1} - m_U} Q(U) + V(i, U).
+    float m = mlo;
+    for (int U = lo; U < hi; ++U) {
+        const float mn = (U + 1 < hi) ? col[(int64_t)(U + 1) * NB] : mhi;
+        q = fmaf(fexp2(mn - m), q, V[U]);
+        col[(int64_t)(U + 1) * NB] = q;
+        m = mn;
+    }
+}
+
 // Dynamic LDS: sBM, scanA, scanB, NB floats each.
 __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) {
     extern __shared__ float dyn[];
@@ -169,7 +244,11 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
         // cmid(ib, jb) = max(A_jb, c_U, B_ib), A_jb = max over (jb, U) = scanA[jb + 1],
         // B_ib = max over (U, ib) = scanB[ib - 1].  Consecutive threads read consecutive jb.
         float acc = 0.f;
-        if (npairs <= NTHREADS) {  // uniform: one pair per thread at most
+        if (NB >= MID_SCAN_NB) {  // uniform: S_U 2^{c_U} = sum_{i > U} Q_i(U) 2^{c_U - m_U(i)}
+            const float *qrow = p.tbuf + (brow + U) * NB;  // Q_i(U) at column i of row U
+            for (int ib = U + 1 + tid; ib < NB; ib += NTHREADS)
+                acc += fexp2(cU - fmaxf(cU, scanB[ib - 1])) * qrow[ib];
+        } else if (npairs <= NTHREADS) {  // uniform: one pair per thread at most
             if (tid < npairs) {
                 const int ib = U + 1 + tid / U, jb = tid % U;
                 const float cm = fmaxf(fmaxf(scanA[jb + 1], cU), scanB[ib - 1]);
@@ -379,6 +458,12 @@ hipError_t launch_bwd_combine(const BwdParams &p, hipStream_t s) {
                                                            hipFuncAttributeMaxDynamicSharedMemorySize,
                                                            3 * MAX_NB * (int)sizeof(float));
         if (attr != hipSuccess) return attr;
+    }
+    if (p.NB >= MID_SCAN_NB) {
+        hipLaunchKernelGGL(fpa_bwd_mid_kernel, head_grid((p.NB + NTHREADS / 64 - 1) / (NTHREADS / 64), p.H, p.BH),
+                           dim3(NTHREADS), 0, s, p);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
     }
     hipLaunchKernelGGL(fpa_bwd_combine_kernel, head_grid(p.NB, p.H, p.BH), dim3(NTHREADS), dyn, s, p);
     return hipGetLastError();
