@@ -85,8 +85,9 @@ __device__ __forceinline__ float block_sum_256(float x, float *red, int w, int l
 // From this many blocks per head on, the middle-block sums run in O(NB^2) per head: the mid kernel
 // below turns each row of TBUF into prefix sums first, and the combine reads one sum per query block.
 // Below it the combine sums every (query block, key block) pair around each block, O(NB^3 / 6) per
-// head, which costs less than a second launch.
-constexpr int MID_SCAN_NB = 128;
+// head, which costs less than a second launch (measured: the two break even between 128 and 192
+// blocks at H12).
+constexpr int MID_SCAN_NB = 160;
 
 // Row i (query block) of a head's TBUF holds V(i, j) = 2^{cmid(i, j)} M(i, j) for key blocks j <= i - 2,
 // M(i, j) the middle-block soft-min sum of the block pair and cmid(i, j) = max a over blocks j+1 .. i-1.

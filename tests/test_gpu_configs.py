@@ -110,3 +110,18 @@ def test_cfg4_full_length(fpa):
     del again
     ref = O.fpa_grads_chunked(*inp, device="cuda")
     compare("cfg4", kern, ref, torch.float16)
+
+
+@pytest.mark.parametrize("T", [159 * 64 + 1, 160 * 64 - 5, 192 * 64 + 33])
+def test_middle_block_sums_both_ways(fpa, T):
+    """The middle-block soft-min sums of dphi are taken over every (query block, key block) pair
+    around each block up to 159 blocks per head, and from per-row prefix sums of the middle-block
+    table (a separate pass over each row) from 160 blocks on: both sides of the switch and one
+    length well past it, each with a ragged last block, drift (range minima from deep prefixes) and
+    beta of either sign, in fp32 against the float64 oracle."""
+    _say(f"[mid] B1 H3 T{T} D16 fp32, beta (0.8, -0.6, 1.4), drift 0.01")
+    q, k, v, phi, psi, _, do = O.make_inputs(1, 3, T, 16, dtype=torch.float32, seed=T, drift=0.01)
+    beta = torch.tensor([0.8, -0.6, 1.4])
+    kern = run_hip(fpa, q, k, v, phi, psi, beta, do)
+    ref = O.fpa_grads_chunked(q, k, v, phi, psi, beta, do, device="cuda")
+    compare(f"mid T{T}", kern, ref, torch.float32)
