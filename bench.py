@@ -20,7 +20,8 @@ clones of the six inputs, forward, backward) beside it.
 The default run adds, under ``configs``, the other BASELINE.json workloads: cfg3 and cfg4 (forward and
 forward+backward ms, % of the dtype's MFMA peak) and cfg5 (one training step of fpa.lm.FPADecoder: a
 12-layer d768 H12 pre-norm decoder over B8 x T2048 random tokens, fp16 autocast, gradient scaler,
-AdamW; tokens/s).
+AdamW, fused where torch has it; tokens/s; and the forward+backward alone, as BASELINE.json's cfg5
+defines it: ``fwd_bwd_tokens_per_s``).
 
 ``ref_protocol`` repeats the measurement with the reference bench's protocol (its bench.py:11-23,
 50-54): each call timed alone between two HIP events, 3 warm-ups + 15 timed calls, the median, over
@@ -158,14 +159,19 @@ LM = dict(B=8, T=2048, d_model=768, n_heads=12, layers=12, d_mlp=3072, vocab=320
 
 
 def lm_step_ms(steps, warmup):
-    """cfg5: ms per training step of the LM (see the module docstring) and the last loss."""
+    """cfg5: ms per training step of the LM (see the module docstring), the last loss, ms of the
+    forward+backward alone (BASELINE.json's cfg5: one forward+backward, no optimizer step) and the
+    optimizer used."""
     import torch
     from fpa.lm import FPADecoder
 
     dev = torch.device("cuda:0")
     torch.manual_seed(0)
     model = FPADecoder(LM["vocab"], LM["d_model"], LM["n_heads"], LM["layers"], LM["d_mlp"], impl="hip").to(dev)
-    opt = torch.optim.AdamW(model.parameters(), lr=1e-4)
+    try:  # one fused kernel per step for all parameters where this torch build has it
+        opt, opt_name = torch.optim.AdamW(model.parameters(), lr=1e-4, fused=True), "AdamW (fused)"
+    except (RuntimeError, ValueError, TypeError):
+        opt, opt_name = torch.optim.AdamW(model.parameters(), lr=1e-4), "AdamW"
     scaler = torch.amp.GradScaler("cuda")
     g = torch.Generator().manual_seed(0)
     tokens = torch.randint(0, LM["vocab"], (LM["B"], LM["T"] + 1), generator=g).to(dev)
@@ -179,6 +185,13 @@ def lm_step_ms(steps, warmup):
         scaler.update()
         return loss
 
+    def fwd_bwd():
+        with torch.autocast("cuda", dtype=torch.float16):
+            loss = model.loss(tokens)
+        model.zero_grad(set_to_none=True)
+        scaler.scale(loss).backward()
+        return loss
+
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -188,16 +201,17 @@ def lm_step_ms(steps, warmup):
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / steps
     loss = loss.item()
+    fb_ms = time_steps(fwd_bwd, steps, warmup)
     del model, opt
     torch.cuda.empty_cache()
-    return ms, loss
+    return ms, loss, fb_ms, opt_name
 
 
 def run_lm(a):
     """--workload lm: the cfg5 training step as the bench line."""
     import torch
     torch.cuda.set_device(0)
-    ms, loss = lm_step_ms(a.steps, a.warmup)
+    ms, loss, fb_ms, opt_name = lm_step_ms(a.steps, a.warmup)
     ntok = LM["B"] * LM["T"]
     res = {
         "metric": "LM training step tokens/s (cfg5: 12-layer d768 H12 FPA decoder, B8 T2048, fp16 autocast)",
@@ -212,7 +226,9 @@ def run_lm(a):
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic (uniform random tokens, random-init weights)",
-        "config": {"workload": "cfg5: FPADecoder training step (AdamW, grad scaler)", **LM,
+        "fwd_bwd_ms": round(fb_ms, 3),
+        "fwd_bwd_tokens_per_s": round(ntok / (fb_ms * 1e-3), 1),
+        "config": {"workload": f"cfg5: FPADecoder training step ({opt_name}, grad scaler)", **LM,
                    "parallelism": "single GPU"},
         "final_loss": round(loss, 4),
         "roofline": None,
@@ -460,10 +476,13 @@ def main():
             if name != a.config:
                 extra[name] = time_config(CONFIGS[name], 10, 3)
                 torch.cuda.empty_cache()
-        lm_ms, lm_loss = lm_step_ms(5, 2)
-        extra["cfg5"] = {"workload": "FPADecoder training step: 12 layers d768 H12, B8 T2048, fp16 autocast, AdamW",
+        lm_ms, lm_loss, lm_fb_ms, opt_name = lm_step_ms(5, 2)
+        ntok = LM["B"] * LM["T"]
+        extra["cfg5"] = {"workload": f"FPADecoder training step: 12 layers d768 H12, B8 T2048, fp16 autocast, {opt_name}",
                          "ms_per_step": round(lm_ms, 3),
-                         "tokens_per_s": round(LM["B"] * LM["T"] / (lm_ms * 1e-3), 1),
+                         "tokens_per_s": round(ntok / (lm_ms * 1e-3), 1),
+                         "fwd_bwd_ms": round(lm_fb_ms, 3),
+                         "fwd_bwd_tokens_per_s": round(ntok / (lm_fb_ms * 1e-3), 1),
                          "loss": round(lm_loss, 4)}
 
     cpu = cpu1 = None
