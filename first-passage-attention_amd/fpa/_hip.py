@@ -9,9 +9,23 @@ multiple of the block and no ``.contiguous()`` copy for the layer's permuted vie
 a tensor is copied only when its head dimension is not contiguous or its rows are
 not 16-byte aligned.
 """
+import functools
+
 import torch
 
 from . import _lib
+
+
+@functools.lru_cache(maxsize=256)
+def _fwd_floats(B, H, T):
+    """(lse floats, state floats) of a forward of this shape."""
+    L = _lib.lib()
+    return L.fpa_lse_floats(B, H, T), L.fpa_state_floats(B, H, T)
+
+
+@functools.lru_cache(maxsize=256)
+def _bwd_ws_bytes(B, H, T, D, dtype):
+    return _lib.lib().fpa_bwd_workspace_bytes(B, H, T, D, dtype)
 
 
 def _rows_ok(t):
@@ -30,12 +44,12 @@ class FwdBuffers:
     """Outputs and saved state of one forward call (all allocated by torch on q's device)."""
 
     def __init__(self, q, o=None):
-        L = _lib.lib()
         B, H, T, D = q.shape
         dev = q.device
         self.o = torch.empty((B, H, T, D), dtype=q.dtype, device=dev) if o is None else o
-        self.lse = torch.empty(L.fpa_lse_floats(B, H, T), dtype=torch.float32, device=dev)
-        self.state = torch.empty(L.fpa_state_floats(B, H, T), dtype=torch.float32, device=dev)
+        n_lse, n_state = _fwd_floats(B, H, T)
+        both = torch.empty(n_lse + n_state, dtype=torch.float32, device=dev)  # one allocation, two regions
+        self.lse, self.state = both[:n_lse], both[n_lse:]
 
 
 # Backward scratch kept per (device, stream) and grown on demand: a backward's kernels run in
@@ -66,7 +80,6 @@ class BwdBuffers:
     """Gradients and scratch of one backward call."""
 
     def __init__(self, q, dqkv=None):
-        L = _lib.lib()
         B, H, T, D = q.shape
         dev = q.device
         if dqkv is None:
@@ -78,7 +91,7 @@ class BwdBuffers:
         self.dphi = torch.empty((B, H, T), dtype=torch.float32, device=dev)
         self.dpsi = torch.empty_like(self.dphi)
         self.dbeta = torch.empty(H, dtype=torch.float32, device=dev)
-        self.ws = workspace(dev, L.fpa_bwd_workspace_bytes(B, H, T, D, _lib.dtype_code(q.dtype)))
+        self.ws = workspace(dev, _bwd_ws_bytes(B, H, T, D, _lib.dtype_code(q.dtype)))
 
 
 def fwd_args(q, k, v, phi, psi, beta, tau, out):

@@ -132,12 +132,20 @@ def dtype_code(dt):
     raise ValueError("q, k and v must all be fp16 or all fp32")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(device):
+    """torch's current stream on `device`, as the C ABI's stream argument."""
+    if _raw_stream is not None:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        return ctypes.c_void_p(_raw_stream(idx))
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
 def ptr(t):
-    return ctypes.c_void_p(t.data_ptr())
+    """Device address of t for a pointer field of an argument struct (an int: ctypes converts it)."""
+    return t.data_ptr()
 
 
 def strides4(t):
