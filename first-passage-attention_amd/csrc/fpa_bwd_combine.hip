@@ -23,6 +23,9 @@
 // instead of the chains' exponentials), and the key-block and query-block parts become sums of
 // per-position terms 2^{c_U - C_s} W_s and 2^{c_U - c_t} R_t times 2^{a_u - c_U}.
 //
+// The middle-block sum runs over every pair (i, j) around U (below MID_SCAN_NB blocks per head) or
+// over the prefix sums that fpa_bwd_mid_kernel leaves per query block i (from MID_SCAN_NB on).
+//
 // dbeta[h] is summed (fixed order) by the workgroup of block 0 of batch 0 of head h.
 // All sums run in a fixed order: the result is bit-reproducible.
 #include "fpa_common.h"
