@@ -460,6 +460,8 @@ def main():
     }
     for name, phases, flops in BWD_KERNELS:
         kernels[name] = (time_call(ba, _hip.run_bwd, phases), flops * D * P)
+    if fb.ws is not None:  # split row tiles: their merge (reads and rewrites o, so timed after the rest)
+        kernels["fpa_fwd_merge"] = (time_call(fa, _hip.run_fwd, _lib.FPA_FWD_MERGE), 0)
     dom = max(kernels, key=lambda n: kernels[n][0])
     dom_ms, dom_flops = kernels[dom]
     peak = PEAK_TFLOPS[cfg["dtype"]]

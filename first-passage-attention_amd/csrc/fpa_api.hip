@@ -109,6 +109,26 @@ int hip_fail(hipError_t e, const char *where) {
     return fail(FPA_ERR_HIP, std::string(where) + ": " + hipGetErrorString(e));
 }
 
+// Forward scratch: part A's normalised output of the split rows (q's type), then four floats per
+// split row (running maximum and sum of parts B and A).  ns = 0: no split, no scratch.
+struct FwdWs {
+    int ns = 0;
+    int64_t rs0 = 0, obytes = 0, total = 0;  // bytes
+};
+
+FwdWs fwd_ws(int64_t B, int64_t H, int64_t T, int64_t D, int32_t dtype) {
+    FwdWs f;
+    if (B < 1 || H < 1 || T < 1 || (dtype != FPA_F16 && dtype != FPA_F32) || !supported_d(dtype, (int)D)) return f;
+    f.ns = fwd_split_tiles(B * H, T, dtype, (int)D);
+    if (f.ns == 0) return f;
+    const int64_t BM = 32 * FPA_NW, nqt = (T + BM - 1) / BM;
+    f.rs0 = (nqt - f.ns) * BM;
+    const int64_t rows = B * H * (T - f.rs0);
+    f.obytes = (rows * D * (dtype == FPA_F16 ? 2 : 4) + 255) / 256 * 256;
+    f.total = f.obytes + rows * 16;
+    return f;
+}
+
 }  // namespace
 
 #ifndef FPA_SOURCE_HASH
@@ -117,7 +137,7 @@ int hip_fail(hipError_t e, const char *where) {
 
 extern "C" {
 
-int fpa_abi_version(void) { return 4; }
+int fpa_abi_version(void) { return 5; }
 
 const char *fpa_source_hash(void) { return FPA_SOURCE_HASH; }
 
@@ -129,6 +149,10 @@ int64_t fpa_state_floats(int64_t B, int64_t H, int64_t T) {
 }
 
 int64_t fpa_lse_floats(int64_t B, int64_t H, int64_t T) { return 2 * B * H * tp_of(T); }
+
+int64_t fpa_fwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D, int32_t dtype) {
+    return fwd_ws(B, H, T, D, dtype).total;
+}
 
 int64_t fpa_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D, int32_t dtype) {
     (void)D;
@@ -193,6 +217,8 @@ int fpa_fwd(const FpaFwdArgs *a, void *stream) {
         return fail(FPA_ERR_INVALID, "the head dimension of q, k, v and o must be contiguous");
     if (!a->phi || !a->psi || !a->beta || !a->lse || !a->state)
         return fail(FPA_ERR_INVALID, "phi, psi, beta, lse and state must be non-NULL");
+    if ((reinterpret_cast<uintptr_t>(a->workspace) & 255) != 0)
+        return fail(FPA_ERR_INVALID, "workspace must be 256-byte aligned");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int64_t TP = tp_of(a->T);
     StatsParams sp;
@@ -202,7 +228,7 @@ int fpa_fwd(const FpaFwdArgs *a, void *stream) {
     sp.state = a->state;
     sp.H = (int)a->H; sp.T = (int)a->T; sp.TP = (int)TP; sp.NB = (int)(TP / G); sp.BH = (int)(a->B * a->H);
     sp.il2 = LOG2E / a->tau;
-    const int ph = a->phases ? a->phases : (FPA_FWD_STATS | FPA_FWD_MAIN);
+    const int ph = a->phases ? a->phases : (FPA_FWD_STATS | FPA_FWD_MAIN | FPA_FWD_MERGE);
     hipError_t e;
     if ((ph & FPA_FWD_STATS) && (e = launch_stats(sp, s)) != hipSuccess) return hip_fail(e, "fpa_stats launch");
     FwdParams fp;
@@ -213,8 +239,15 @@ int fpa_fwd(const FpaFwdArgs *a, void *stream) {
     fp.beta = a->beta; fp.lse = a->lse; fp.state = a->state;
     fp.H = sp.H; fp.T = sp.T; fp.TP = sp.TP; fp.NB = sp.NB; fp.BH = sp.BH;
     fp.sc2 = LOG2E / sqrtf((float)a->D);
+    const FwdWs fw = a->workspace ? fwd_ws(a->B, a->H, a->T, a->D, a->dtype) : FwdWs{};
+    fp.ns = fw.ns;
+    fp.rs0 = (int)fw.rs0;
+    fp.ows = fw.ns ? a->workspace : nullptr;
+    fp.oml = fw.ns ? reinterpret_cast<float *>(static_cast<char *>(a->workspace) + fw.obytes) : nullptr;
     if ((ph & FPA_FWD_MAIN) && (e = launch_fwd(fp, a->dtype, (int)a->D, s)) != hipSuccess)
         return hip_fail(e, "fpa_fwd launch");
+    if (fp.ns && (ph & FPA_FWD_MERGE) && (e = launch_fwd_merge(fp, a->dtype, (int)a->D, s)) != hipSuccess)
+        return hip_fail(e, "fpa_fwd_merge launch");
     return FPA_OK;
 }
 

@@ -32,6 +32,13 @@
 #ifndef FPA_FWD_SNAKE
 #define FPA_FWD_SNAKE 1
 #endif
+// Split the key range of the heaviest half of the row tiles when the launch's workgroups fill at most
+// this percentage of the slots (CUs x workgroups per CU); 0 never splits.  Measured on MI355X at
+// T = 2048, D = 64 fp16: at half the slots (B2 H12) the split forward with its merge takes 40 against
+// 47 us; at one or two full rounds (B4, B8 H12; B2 H8 T4096 fp32) it is 8-16% slower.
+#ifndef FPA_FWD_SPLIT_FILL
+#define FPA_FWD_SPLIT_FILL 50
+#endif
 
 namespace fpa {
 
@@ -68,8 +75,17 @@ fpa_fwd_kernel(FwdParams p) {
     const int tid = thread_x(), lane = tid % 64, g = lane / 32, c = lane % 32;
     const int w = __builtin_amdgcn_readfirstlane(tid / 64);  // wave index, uniform across the wave
     const int nqt = (p.T + BM - 1) / BM;
-    int rank, bh;
-    xcd_work_item(rank, bh, p.BH, p.H, nqt, FPA_FWD_SNAKE ? WPE : 1);
+    // Item k of a head (0 the heaviest): with ns split row tiles (rank r < ns, rank 0 the last rows),
+    // items 3i and 3i + 1 are parts B and A of rank i and item 3i + 2 is the whole of rank ns + i; the
+    // items after 3 ns are ranks 2 ns, 2 ns + 1, ... (nqt >= 2 ns).  part 0: every key of the rows.
+    int k, bh;
+    xcd_work_item(k, bh, p.BH, p.H, nqt + p.ns, FPA_FWD_SNAKE ? WPE : 1);
+    int rank = k - p.ns, part = 0;
+    if (k < 3 * p.ns) {
+        const int i = k / 3, j = k - 3 * i;
+        rank = (j == 2) ? p.ns + i : i;
+        part = (j == 2) ? 0 : j + 1;
+    }
     const int qt = nqt - 1 - rank;  // longest rows first
     const int b = bh / p.H, h = bh % p.H;
     const int q0 = qt * BM, qw0 = q0 + 32 * w, tq = qw0 + c;
@@ -109,7 +125,12 @@ fpa_fwd_kernel(FwdParams p) {
 
     const int nkt = (p.T + BN - 1) / BN;
     const int jtmax = umin_i(nkt - 1, (q0 + BM - 1) / BN);
-    issue(jtmax, 0);
+    // Key tiles of this item: part B takes jsplit .. jtmax (every diagonal block of the rows: jsplit
+    // <= qt + 1 <= 2 qt for the split tiles, qt >= 1), part A the tiles below jsplit, all before q0.
+    const int jsplit = (jtmax + 1) >> 1;
+    const int jhi = (part == 2) ? jsplit - 1 : jtmax;
+    const int jlo = (part == 1) ? jsplit : 0;
+    issue(jhi, 0);
 
     OpRow<T, D> qreg;
     load_row_p1<T, D>(qreg, Qb + (int64_t)tq * p.sq.t, tq < p.T, g);
@@ -123,10 +144,15 @@ fpa_fwd_kernel(FwdParams p) {
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) oacc[dt] = zero16();
     float mid = pinf();  // min phi over the blocks strictly between the key block and ib
+    if (part == 2 && wave_active) {  // part A starts below block jsplit: mid covers blocks jsplit .. ib - 1
+        const float *bmin = p.state + L.bplane(BP_MIN) + (int64_t)bh * p.NB;
+        for (int j0 = jsplit; j0 < ib; j0 += 64) mid = fminf(mid, (j0 + lane < ib) ? bmin[j0 + lane] : pinf());
+        mid = wave_min(mid);
+    }
 
     wait_loads();
     __syncthreads();
-    for (int jt = jtmax, it = 0; jt >= 0; --jt, ++it) {
+    for (int jt = jhi, it = 0; jt >= jlo; --jt, ++it) {
         const int buf = (NS == 2) ? (it & 1) : 0;
         const int s0 = jt * BN;
         if constexpr (NS == 2) issue_full(jt > 0 ? jt - 1 : 0, buf ^ 1);
@@ -246,8 +272,12 @@ fpa_fwd_kernel(FwdParams p) {
 
     if (!wave_active) return;
     const float inv = 1.f / l_i;
+    // Split rows: the part's output normalised by its own sum (part B into o, part A into ows) and its
+    // running maximum and sum (oml); the merge kernel writes the rows' o and lse.
+    const int64_t srow = (int64_t)bh * (p.T - p.rs0) + (tq - p.rs0);
     if (tq < p.T) {
-        T *Orow = static_cast<T *>(p.o) + b * p.so.b + h * p.so.h + (int64_t)tq * p.so.t;
+        T *Orow = (part == 2) ? static_cast<T *>(p.ows) + srow * D
+                              : static_cast<T *>(p.o) + b * p.so.b + h * p.so.h + (int64_t)tq * p.so.t;
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
@@ -266,6 +296,13 @@ fpa_fwd_kernel(FwdParams p) {
                 }
             }
     }
+    if (part != 0) {  // rows past T (up to TP) get the whole-row values from part B
+        if (tq < p.T) {
+            if (g == 0) *reinterpret_cast<f32x2 *>(p.oml + 4 * srow + 2 * (part - 1)) = f32x2{m_i, l_i};
+            return;
+        }
+        if (part == 2) return;
+    }
     if (g == 0 && tq < p.TP) {
         if constexpr (XB) {  // fp32: the running maximum and log2 l, for the backward's P = 2^{(s - m) - log2 l}
             p.lse[rowbase + tq] = m_i;
@@ -276,15 +313,67 @@ fpa_fwd_kernel(FwdParams p) {
     }
 }
 
+// Rows of a split row tile: o = (wB oB + wA oA) / (wB + wA) with w = l 2^{m - max(mA, mB)} from the two
+// parts' normalised outputs, and the row's lse (fp32: the running maximum and log2 of the sum).  One
+// thread per 16-byte chunk of a row.
+template <typename T, int D>
+__global__ void __launch_bounds__(256) fpa_fwd_merge_kernel(FwdParams p) {
+    constexpr int CH = 16 / (int)sizeof(T), CPR = D / CH;  // elements per chunk, chunks per row
+    const int64_t nsr = p.T - p.rs0;
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t row = gid / CPR;
+    if (row >= (int64_t)p.BH * nsr) return;
+    const int ch = (int)(gid - row * CPR);
+    const int bh = (int)(row / nsr), t = p.rs0 + (int)(row - (int64_t)bh * nsr);
+    const int b = bh / p.H, h = bh % p.H;
+    const f32x4 ml = *reinterpret_cast<const f32x4 *>(p.oml + 4 * row);
+    const float m = fmaxf(ml[0], ml[2]);
+    const float wb = ml[1] * fexp2(ml[0] - m), wa = ml[3] * fexp2(ml[2] - m);
+    const float l = wa + wb, inv = 1.f / l;
+    T *orow = static_cast<T *>(p.o) + b * p.so.b + h * p.so.h + (int64_t)t * p.so.t + ch * CH;
+    const T *arow = static_cast<const T *>(p.ows) + row * D + ch * CH;
+    if constexpr (sizeof(T) == 2) {
+        h8 ob = *reinterpret_cast<const h8 *>(orow), oa = *reinterpret_cast<const h8 *>(arow), out;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) out[e] = (f16)(((float)ob[e] * wb + (float)oa[e] * wa) * inv);
+        *reinterpret_cast<h8 *>(orow) = out;
+    } else {
+        f32x4 ob = *reinterpret_cast<const f32x4 *>(orow), oa = *reinterpret_cast<const f32x4 *>(arow), out;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) out[e] = (ob[e] * wb + oa[e] * wa) * inv;
+        *reinterpret_cast<f32x4 *>(orow) = out;
+    }
+    if (ch == 0) {
+        const int64_t li = (int64_t)bh * p.TP + t;
+        if constexpr (exact_bias<T>()) {
+            p.lse[li] = m;
+            p.lse[(int64_t)p.BH * p.TP + li] = flog2(l);
+        } else {
+            p.lse[li] = m + flog2(l);
+        }
+    }
+}
+
+template <typename T, int D>
+constexpr int fwd_wpe() { return (D >= 128) ? 1 : (sizeof(T) == 2 ? FPA_FWD_WPE : FPA_FWD_WPE32); }
+
 template <typename T, int D>
 static hipError_t launch_fwd_t(const FwdParams &p, hipStream_t s) {
-    constexpr int NW = FPA_NW, WPE = (D >= 128) ? 1 : (sizeof(T) == 2 ? FPA_FWD_WPE : FPA_FWD_WPE32);
+    constexpr int NW = FPA_NW, WPE = fwd_wpe<T, D>();
     const int nqt = (p.T + 32 * NW - 1) / (32 * NW);
-    hipLaunchKernelGGL((fpa_fwd_kernel<T, D, WPE, NW>), head_grid(nqt, p.H, p.BH), dim3(64 * NW), 0, s, p);
+    hipLaunchKernelGGL((fpa_fwd_kernel<T, D, WPE, NW>), head_grid(nqt + p.ns, p.H, p.BH), dim3(64 * NW), 0, s, p);
+    return hipGetLastError();
+}
+
+template <typename T, int D>
+static hipError_t launch_fwd_merge_t(const FwdParams &p, hipStream_t s) {
+    const int64_t threads = (int64_t)p.BH * (p.T - p.rs0) * (D / (16 / (int)sizeof(T)));
+    hipLaunchKernelGGL((fpa_fwd_merge_kernel<T, D>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, p);
     return hipGetLastError();
 }
 
 // fp16 instantiations (fpa_fwd16.hip).
 hipError_t launch_fwd_f16(const FwdParams &p, int D, hipStream_t s);
+hipError_t launch_fwd_merge_f16(const FwdParams &p, int D, hipStream_t s);
 
 }  // namespace fpa

@@ -80,6 +80,25 @@ hipError_t launch_stats(const StatsParams &p, hipStream_t s) {
     return hipGetLastError();
 }
 
+int fwd_split_tiles(int64_t BH, int64_t T, int dtype, int D) {
+    const int64_t nqt = (T + 32 * FPA_NW - 1) / (32 * FPA_NW);
+    const int wpe = (D >= 128) ? 1 : (dtype == 0 ? FPA_FWD_WPE : FPA_FWD_WPE32);
+    if (nqt < 4 || 100 * BH * nqt > (int64_t)FPA_FWD_SPLIT_FILL * 8 * XCD_CUS * wpe) return 0;
+    return (int)(nqt / 2);
+}
+
+hipError_t launch_fwd_merge(const FwdParams &p, int dtype, int D, hipStream_t s) {
+    if (dtype == 0) return launch_fwd_merge_f16(p, D, s);
+    switch (D) {
+        case 16: return launch_fwd_merge_t<float, 16>(p, s);
+        case 32: return launch_fwd_merge_t<float, 32>(p, s);
+        case 64: return launch_fwd_merge_t<float, 64>(p, s);
+        case 128: return launch_fwd_merge_t<float, 128>(p, s);
+        case 256: return launch_fwd_merge_t<float, 256>(p, s);
+    }
+    return hipErrorInvalidValue;
+}
+
 hipError_t launch_fwd(const FwdParams &p, int dtype, int D, hipStream_t s) {
     if (dtype == 0) return launch_fwd_f16(p, D, s);
     switch (D) {

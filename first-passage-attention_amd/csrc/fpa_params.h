@@ -30,6 +30,12 @@ struct FwdParams {
     const float *state;  // block statistics
     int H, T, TP, NB, BH;
     float sc2;           // log2(e) / sqrt(D)
+    // Split rows: the ns heaviest row tiles of each head (rows rs0 .. T-1) run as two items, the keys
+    // from the middle tile up to the diagonal (part B: its normalised output goes to o) and the keys
+    // below (part A: to ows); fpa_fwd_merge_kernel combines them.  ns = 0: no split.
+    void *ows;           // BH * (T - rs0) * D elements of q's type: part A's normalised output
+    float *oml;          // BH * (T - rs0) * 4: running maximum and sum of part B, then of part A
+    int ns, rs0;
 };
 
 struct BwdParams {
@@ -87,6 +93,9 @@ __host__ __device__ inline int64_t qi_at(int64_t bh, int NB, int row, int plane)
 // Launchers (defined next to their kernels); return hipSuccess or the launch error.
 hipError_t launch_stats(const StatsParams &p, hipStream_t s);
 hipError_t launch_fwd(const FwdParams &p, int dtype, int D, hipStream_t s);
+hipError_t launch_fwd_merge(const FwdParams &p, int dtype, int D, hipStream_t s);
+// Row tiles per head that the forward splits (0: none) for a (BH, T) problem.
+int fwd_split_tiles(int64_t BH, int64_t T, int dtype, int D);
 hipError_t launch_bwd_prep(const BwdParams &p, int dtype, int D, hipStream_t s);
 hipError_t launch_bwd_kv(const BwdParams &p, int dtype, int D, hipStream_t s);
 hipError_t launch_bwd_q(const BwdParams &p, int dtype, int D, hipStream_t s);

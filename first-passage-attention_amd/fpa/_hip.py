@@ -28,6 +28,11 @@ def _bwd_ws_bytes(B, H, T, D, dtype):
     return _lib.lib().fpa_bwd_workspace_bytes(B, H, T, D, dtype)
 
 
+@functools.lru_cache(maxsize=256)
+def _fwd_ws_bytes(B, H, T, D, dtype):
+    return _lib.lib().fpa_fwd_workspace_bytes(B, H, T, D, dtype)
+
+
 def _rows_ok(t):
     ce = 8 if t.dtype == torch.float16 else 4
     s = t.stride()
@@ -50,17 +55,20 @@ class FwdBuffers:
         n_lse, n_state = _fwd_floats(B, H, T)
         both = torch.empty(n_lse + n_state, dtype=torch.float32, device=dev)  # one allocation, two regions
         self.lse, self.state = both[:n_lse], both[n_lse:]
+        # Scratch of the split row tiles (none for most shapes), needed only while the call runs.
+        nws = _fwd_ws_bytes(B, H, T, D, _lib.dtype_code(q.dtype))
+        self.ws = workspace(dev, nws) if nws else None
 
 
-# Backward scratch kept per (device, stream) and grown on demand: a backward's kernels run in
-# stream order, so the next backward on the same stream may reuse the same bytes.  Under HIP graph
+# Scratch kept per (device, stream) and grown on demand: a call's kernels run in stream order, so
+# the next forward or backward on the same stream may reuse the same bytes.  Under HIP graph
 # capture a fresh tensor is taken instead (from the graph's private pool, alive as long as the
 # graph), so a later growth of the cache never frees memory that a captured graph still uses.
 _WS_CACHE = {}
 
 
 def workspace(dev, nbytes):
-    """A uint8 device tensor of at least nbytes for one backward call on the current stream."""
+    """A uint8 device tensor of at least nbytes for one forward or backward call on the current stream."""
     if torch.cuda.is_current_stream_capturing():
         return torch.empty(nbytes, dtype=torch.uint8, device=dev)
     key = (dev.index if dev.index is not None else torch.cuda.current_device(), torch.cuda.current_stream(dev).cuda_stream)
@@ -110,6 +118,7 @@ def fwd_args(q, k, v, phi, psi, beta, tau, out):
     a.o, a.so = _lib.ptr(out.o), _lib.strides4(out.o)
     a.lse, a.state = _lib.ptr(out.lse), _lib.ptr(out.state)
     a.phases = 0
+    a.workspace = _lib.ptr(out.ws) if out.ws is not None else None
     return a
 
 

@@ -12,12 +12,12 @@ import torch
 
 from ._srchash import source_hash
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libfpa.so")
 
 FPA_F16, FPA_F32 = 0, 1
 FPA_OK, FPA_ERR_INVALID, FPA_ERR_UNSUPPORTED, FPA_ERR_HIP = 0, 1, 2, 3
-FPA_FWD_STATS, FPA_FWD_MAIN = 1, 2
+FPA_FWD_STATS, FPA_FWD_MAIN, FPA_FWD_MERGE = 1, 2, 4
 FPA_BWD_DELTA, FPA_BWD_KEYS, FPA_BWD_QUERIES, FPA_BWD_PHI, FPA_BWD_BETA = 1, 2, 4, 8, 16
 NOALLOC_SCRATCH_BYTES = 64 << 20  # FPA_NOALLOC_SCRATCH_BYTES of include/fpa.h
 
@@ -33,7 +33,7 @@ class FpaFwdArgs(ctypes.Structure):
                 ("q", _vp), ("sq", _S4), ("k", _vp), ("sk", _S4), ("v", _vp), ("sv", _S4),
                 ("phi", _vp), ("sphi", _S3), ("psi", _vp), ("spsi", _S3),
                 ("beta", _vp), ("o", _vp), ("so", _S4), ("lse", _vp), ("state", _vp),
-                ("phases", ctypes.c_int32)]
+                ("phases", ctypes.c_int32), ("workspace", _vp)]
 
 
 class FpaBwdArgs(ctypes.Structure):
@@ -87,8 +87,9 @@ def lib():
     for name in ("fpa_state_floats", "fpa_lse_floats"):
         getattr(L, name).restype = _i64
         getattr(L, name).argtypes = [_i64, _i64, _i64]
-    L.fpa_bwd_workspace_bytes.restype = _i64
-    L.fpa_bwd_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64, ctypes.c_int32]
+    for name in ("fpa_fwd_workspace_bytes", "fpa_bwd_workspace_bytes"):
+        getattr(L, name).restype = _i64
+        getattr(L, name).argtypes = [_i64, _i64, _i64, _i64, ctypes.c_int32]
     L.fpa_fwd.restype = ctypes.c_int
     L.fpa_fwd.argtypes = [ctypes.POINTER(FpaFwdArgs), _vp]
     L.fpa_bwd.restype = ctypes.c_int

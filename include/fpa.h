@@ -17,6 +17,8 @@
  *               delta, key side, query side, phi/beta combine);
  *   fpa_state_floats / fpa_bwd_workspace_bytes <- the scratch allocations of
  *               kernel.py:390-392, 406-407, 430-436, sized so the caller owns them;
+ *   fpa_fwd_workspace_bytes: no counterpart in the reference (the scratch of this
+ *               forward's split row tiles, see FpaFwdArgs.workspace);
  *   fpa_field_fwd <- Field.forward (kernel.py:502-509): the fp32 projection of x
  *               to (delta, g, h), W = cumsum_t delta, phi = W + g, psi = W + h;
  *   fpa_field_bwd <- the autograd backward of those operations (dx, dW, dbias
@@ -41,6 +43,7 @@ extern "C" {
 /* phase bits (FpaFwdArgs.phases / FpaBwdArgs.phases) */
 #define FPA_FWD_STATS 1    /* block statistics of phi                      */
 #define FPA_FWD_MAIN 2     /* the forward kernel (o, lse)                  */
+#define FPA_FWD_MERGE 4    /* o and lse of the split row tiles             */
 #define FPA_BWD_DELTA 1    /* Delta_t = sum_d dO o                         */
 #define FPA_BWD_KEYS 2     /* key side: dk, dv, dpsi, dbeta partials, ...  */
 #define FPA_BWD_QUERIES 4  /* query side: dq, query-block soft-min sums;
@@ -76,7 +79,15 @@ typedef struct {
     float *lse;
     float *state;
     int32_t phases;  /* 0: everything.  Otherwise a bitmask of the kernels to enqueue
-                        (FPA_FWD_STATS | FPA_FWD_MAIN), for per-kernel timing only. */
+                        (FPA_FWD_STATS | FPA_FWD_MAIN | FPA_FWD_MERGE), for per-kernel
+                        timing only. */
+    void *workspace; /* fpa_fwd_workspace_bytes(...) bytes of device memory, 256-byte
+                        aligned, contents on entry irrelevant; or NULL.  When the launch
+                        would be short of workgroups, the heaviest row tiles are split in
+                        two halves of their key range that run side by side, and a merge
+                        kernel combines them through this scratch; with NULL (or a shape
+                        that needs none) every row tile runs whole.  Same results up to
+                        rounding either way.  Needed only until the call's work ends.  */
 } FpaFwdArgs;
 
 /* Backward arguments: the forward's inputs, o, lse and state, the incoming
@@ -151,6 +162,10 @@ int64_t fpa_state_floats(int64_t B, int64_t H, int64_t T);
 
 /* Floats of lse for a (B, H, T) problem (2 * B * H * TP). */
 int64_t fpa_lse_floats(int64_t B, int64_t H, int64_t T);
+
+/* Bytes of forward scratch for a (B, H, T, D) problem: 0 when its forward splits no
+ * row tile (see FpaFwdArgs.workspace). */
+int64_t fpa_fwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D, int32_t dtype);
 
 /* Bytes of backward scratch for a (B, H, T, D) problem. */
 int64_t fpa_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D, int32_t dtype);

@@ -135,6 +135,53 @@ def test_fused_backward_matches_separate_launches(fpa):
         assert all(torch.equal(x, y) for x, y in zip(*outs))
 
 
+SPLIT_CASES = [  # (B, H, T, D, dtype, beta, seed): shapes whose forward splits its heaviest row tiles
+    (1, 3, 1000, 32, torch.float16, (-0.7, 0.0, 1.3), 41),
+    (3, 5, 777, 16, torch.float32, None, 42),
+    (1, 1, 4100, 128, torch.float16, None, 43),
+    (2, 1, 600, 256, torch.float32, None, 44),
+    (1, 2, 700, 64, torch.float16, None, 45),
+]
+
+
+@pytest.mark.parametrize("B,H,T,D,dtype,beta,seed", SPLIT_CASES)
+def test_split_forward(fpa, B, H, T, D, dtype, beta, seed):
+    """When the launch is short of workgroups the forward runs the heaviest row tiles as two halves of
+    their key range and a merge kernel combines them.  Without a workspace every row tile runs
+    whole: o agrees to rounding (each half rounds its P and its normalised o on its own) and so does
+    the row's lse (m + log2 l).  Through the split path o agrees with the float64 oracle and, for
+    fp16, the gradients with the oracle fed the kernel's own stored output (Delta from the fp16 o, as
+    the reference's _bwd_delta takes it, kernel.py:165-174): on the first case that rounding alone
+    moves the exact dbeta by 1.7e-2, with or without the split."""
+    from fpa import _hip, _lib
+    _say(f"[split] B{B} H{H} T{T} D{D} {dtype}")
+    dev = torch.device("cuda")
+    q, k, v, phi, psi, b0, do = O.make_inputs(B, H, T, D, dtype=dtype, seed=seed, psi_noise=1.0)
+    beta = torch.tensor(beta) if beta is not None else b0
+    assert _hip._fwd_ws_bytes(B, H, T, D, _lib.dtype_code(dtype)) > 0
+    qd, kd, vd, pd, sd, bd = (t.to(dev) for t in (q, k, v, phi, psi, beta))
+    outs = []
+    for split in (True, False):
+        fb = _hip.FwdBuffers(qd)
+        fa = _hip.fwd_args(qd, kd, vd, pd, sd, bd, 1.0, fb)
+        assert bool(fa.workspace) and fb.ws is not None
+        if not split:
+            fa.workspace = None
+        _hip.run_fwd(fa, dev)
+        torch.cuda.synchronize()
+        TP = fb.lse.numel() // (2 * B * H)
+        lse = fb.lse.view(2, B * H, TP)[:, :, :T]
+        outs.append((fb.o.clone(), lse[0] + lse[1] if dtype == torch.float32 else lse[0].clone()))
+    (o_s, l_s), (o_w, l_w) = outs
+    assert O.rel_err(o_s.cpu(), o_w.cpu()) <= (1e-3 if dtype == torch.float16 else 1e-6)
+    assert (l_s - l_w).abs().max().item() <= (1e-3 if dtype == torch.float16 else 1e-5 * (1 + l_w.abs().max().item()))
+    kern = run_hip(fpa, q, k, v, phi, psi, beta, do)
+    ref = O.fpa_grads_chunked(q, k, v, phi, psi, beta, do, device="cuda")
+    if dtype == torch.float16:
+        ref = ref[:1] + list(O.fpa_grads_stored(q, k, v, phi, psi, beta, do, o_stored=kern[0])[1:])
+    check(kern, ref, dtype)
+
+
 def test_negative_and_zero_beta(fpa):
     """beta <= 0 flips / removes the bias; the kernels take the sign per head."""
     _say("[parity] beta = (-0.7, 0, 1.3)")
