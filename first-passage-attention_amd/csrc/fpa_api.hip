@@ -86,7 +86,7 @@ int check_common(int64_t B, int64_t H, int64_t T, int64_t D, int32_t dtype, floa
     if (!supported_d(dtype, (int)D))
         return fail(FPA_ERR_UNSUPPORTED, "head dimension " + std::to_string(D) + " is not built (16, 32, 64, 128, 256)");
     if (B > 65535 || H > 65535) return fail(FPA_ERR_UNSUPPORTED, "B and H must each be at most 65535");
-    // The combine kernel holds three floats per 64-block of T in LDS; workgroup counts stay below 2^31.
+    // The backward workspace grows as the square of the block count; workgroup counts stay below 2^31.
     if (tp_of(T) / G > MAX_NB) return fail(FPA_ERR_UNSUPPORTED, "T must be at most " + std::to_string(MAX_NB * G));
     if (B * H * (tp_of(T) / G + 1) >= (int64_t(1) << 31)) return fail(FPA_ERR_UNSUPPORTED, "B * H * T is too large");
     return FPA_OK;

@@ -24,7 +24,8 @@
 // per-position terms 2^{c_U - C_s} W_s and 2^{c_U - c_t} R_t times 2^{a_u - c_U}.
 //
 // The middle-block sum runs over every pair (i, j) around U (below MID_SCAN_NB blocks per head) or
-// over the prefix sums that fpa_bwd_mid_kernel leaves per query block i (from MID_SCAN_NB on).
+// over the prefix sums that fpa_bwd_mid_kernel leaves per query block i (from MID_SCAN_NB on), already
+// scaled to 2^{c_U}: then the combine holds no per-block array and any number of blocks fits.
 //
 // dbeta[h] is summed (fixed order) by the workgroup of block 0 of batch 0 of head h.
 // All sums run in a fixed order: the result is bit-reproducible.
@@ -98,21 +99,29 @@ constexpr int MID_SCAN_NB = 160;
 // m_U = max a over blocks U .. i-1 (c_b = max a over block b), the row's prefix sums
 //   Q_i(U) = 2^{m_U} sum_{j < U} M(i, j),   U = 1 .. i - 1,
 // follow Q_i(U + 1) = 2^{m_{U+1} - m_U} Q_i(U) + V(i, U) from Q_i(0) = 0, every factor at most 1, and
-// S_U = sum_{i > U} 2^{-m_U} Q_i(U).  One wave per row: each lane takes a segment of U, composes the
-// segment's affine map (going down, with m_U as a running maximum), the maps are scanned across the
-// lanes, and each lane reruns its segment upward from the value entering it.  Q_i(U) goes to the
-// upper triangle of the head's TBUF matrix (row U, column i > U), which the key side never writes;
-// its m_U values are parked there between the two passes.
+// S_U 2^{c_U} = sum_{i > U} 2^{c_U - m_U} Q_i(U).  One wave per row: each lane takes a segment of U,
+// composes the segment's affine map (going down, with m_U as a running maximum), the maps are scanned
+// across the lanes, and each lane reruns its segment upward from the value entering it.
+// 2^{c_U - m_U} Q_i(U) (a factor at most 1) goes to the upper triangle of the head's TBUF matrix (row U,
+// column i > U), which the key side never writes; the m_U values are parked there between the two
+// passes.  Up to MID_LDS_NB blocks the c_b of the head are staged in LDS, beyond that read from memory.
+constexpr int MID_LDS_NB = 8192;
+
+template <bool LDS>
 __global__ void __launch_bounds__(NTHREADS) fpa_bwd_mid_kernel(BwdParams p) {
-    __shared__ float cb[MAX_NB];  // c_b for the head's blocks
+    __shared__ float cbs[LDS ? MID_LDS_NB : 1];  // c_b for the head's blocks
     const int bh = group_bh(p.H), tid = thread_x(), lane = tid % 64;
     const int w = __builtin_amdgcn_readfirstlane(tid / 64);
     const int NB = p.NB;
     const int64_t brow = (int64_t)bh * NB;
     const StateLayout L{p.BH, p.TP, p.NB};
+    const float *bmin = p.state + L.bplane(BP_MIN) + brow;
     const int i = __builtin_amdgcn_readfirstlane(group_x() * (NTHREADS / 64) + w);  // this wave's row
-    for (int b = tid; b < NB; b += NTHREADS) cb[b] = -p.state[L.bplane(BP_MIN) + brow + b] * p.il2;
-    __syncthreads();
+    if constexpr (LDS) {
+        for (int b = tid; b < NB; b += NTHREADS) cbs[b] = -bmin[b] * p.il2;
+        __syncthreads();
+    }
+    auto cb = [&](int b) { return LDS ? cbs[b] : -bmin[b] * p.il2; };
     if (i < 2 || i >= NB) return;  // wave-uniform: rows 0 and 1 have no pair
     const float *V = p.tbuf + (brow + i) * NB;  // V(i, U) = V[U], U <= i - 2
     float *col = p.tbuf + brow * NB + i;        // Q_i(U) = col[U * NB]
@@ -120,7 +129,7 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_mid_kernel(BwdParams p) {
     const int k = (n + 63) / 64, lo = min(lane * k, n), hi = min(lo + k, n);
     // m_hi = max(c_hi .. c_{i-1}): the maxima of the later lanes' segments and c_{i-1}.
     float smax = ninf();
-    for (int U = lo; U < hi; ++U) smax = fmaxf(smax, cb[U]);
+    for (int U = lo; U < hi; ++U) smax = fmaxf(smax, cb(U));
     float x = smax;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -129,11 +138,11 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_mid_kernel(BwdParams p) {
     }
     float mhi = __shfl_down(x, 1, 64);
     if (lane == 63) mhi = ninf();
-    mhi = fmaxf(mhi, cb[i - 1]);
+    mhi = fmaxf(mhi, cb(i - 1));
     // Pass 1, down the segment: the composed map Q(hi) = A Q(lo) + B; m_U parked for lo < U < hi.
     float A = 1.f, B = 0.f, mnext = mhi;
     for (int U = hi - 1; U >= lo; --U) {
-        const float m = fmaxf(cb[U], mnext);
+        const float m = fmaxf(cb(U), mnext);
         B = fmaf(V[U], A, B);
         A *= fexp2(mnext - m);
         if (U > lo) col[(int64_t)U * NB] = m;
@@ -151,17 +160,17 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_mid_kernel(BwdParams p) {
     }
     float q = __shfl_up(B, 1, 64);
     if (lane == 0) q = 0.f;
-    // Pass 2, up the segment: Q(U + 1) = 2^{m_{U+1} - m_U} Q(U) + V(i, U).
+    // Pass 2, up the segment: Q(U + 1) = 2^{m_{U+1} - m_U} Q(U) + V(i, U), stored times 2^{c_{U+1} - m_{U+1}}.
     float m = mlo;
     for (int U = lo; U < hi; ++U) {
         const float mn = (U + 1 < hi) ? col[(int64_t)(U + 1) * NB] : mhi;
         q = fmaf(fexp2(mn - m), q, V[U]);
-        col[(int64_t)(U + 1) * NB] = q;
+        col[(int64_t)(U + 1) * NB] = fexp2(cb(U + 1) - mn) * q;
         m = mn;
     }
 }
 
-// Dynamic LDS: sBM, scanA, scanB, NB floats each.
+// Dynamic LDS: sBM, scanA, scanB, NB floats each, below MID_SCAN_NB blocks (none from there on).
 __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) {
     extern __shared__ float dyn[];
     __shared__ float sA[G], sC[G], sc[G], sW[G], sR[G];
@@ -223,7 +232,9 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
             sE[tid] = (tid <= last) ? fexp2(au - cu) : 0.f;
         }
     }
-    for (int i = tid; i < NB; i += NTHREADS) sBM[i] = -p.state[L.bplane(BP_MIN) + brow + i] * il2;
+    const bool midscan = NB >= MID_SCAN_NB;  // uniform
+    if (!midscan)
+        for (int i = tid; i < NB; i += NTHREADS) sBM[i] = -p.state[L.bplane(BP_MIN) + brow + i] * il2;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int q = tid + NTHREADS * i, s = q >> 4, t0 = 4 * (q & 15);
@@ -236,22 +247,23 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
     float gq[16];
 #pragma unroll
     for (int k = 0; k < 16; ++k) gq[k] = contrib[lane][16 * w + k];
-    const float cU = sBM[U];
+    const float cU = -ld_uniform(p.state, L.bplane(BP_MIN) + brow + U) * il2;  // sBM[U]
     const int nI = NB - 1 - U;
     const int npairs = U * nI;
     float SU = 0.f;
     if (npairs > 0) {  // uniform: U is the workgroup's block
         // scanA[i] = max over [i, U), scanB[i] = max over (U, i]; waves 0 and 1 in parallel.
-        if (w == 0) wave_suffix_max(scanA, sBM, NB, U, lane);
-        if (w == 1) wave_prefix_max(scanB, sBM, NB, U, lane);
-        __syncthreads();
+        if (!midscan) {
+            if (w == 0) wave_suffix_max(scanA, sBM, NB, U, lane);
+            if (w == 1) wave_prefix_max(scanB, sBM, NB, U, lane);
+            __syncthreads();
+        }
         // cmid(ib, jb) = max(A_jb, c_U, B_ib), A_jb = max over (jb, U) = scanA[jb + 1],
         // B_ib = max over (U, ib) = scanB[ib - 1].  Consecutive threads read consecutive jb.
         float acc = 0.f;
-        if (NB >= MID_SCAN_NB) {  // uniform: S_U 2^{c_U} = sum_{i > U} Q_i(U) 2^{c_U - m_U(i)}
-            const float *qrow = p.tbuf + (brow + U) * NB;  // Q_i(U) at column i of row U
-            for (int ib = U + 1 + tid; ib < NB; ib += NTHREADS)
-                acc += fexp2(cU - fmaxf(cU, scanB[ib - 1])) * qrow[ib];
+        if (midscan) {  // S_U 2^{c_U} = sum_{i > U} 2^{c_U - m_U(i)} Q_i(U), the terms as the mid pass left them
+            const float *qrow = p.tbuf + (brow + U) * NB;  // at column i of row U
+            for (int ib = U + 1 + tid; ib < NB; ib += NTHREADS) acc += qrow[ib];
         } else if (npairs <= NTHREADS) {  // uniform: one pair per thread at most
             if (tid < npairs) {
                 const int ib = U + 1 + tid / U, jb = tid % U;
@@ -456,16 +468,13 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
 }
 
 hipError_t launch_bwd_combine(const BwdParams &p, hipStream_t s) {
-    const size_t dyn = 3 * (size_t)p.NB * sizeof(float);
-    if (dyn > 48 * 1024) {  // above the default dynamic LDS allowance: raise it once per process
-        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&fpa_bwd_combine_kernel),
-                                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                           3 * MAX_NB * (int)sizeof(float));
-        if (attr != hipSuccess) return attr;
-    }
+    const size_t dyn = (p.NB < MID_SCAN_NB) ? 3 * (size_t)p.NB * sizeof(float) : 0;  // below 2 KB
     if (p.NB >= MID_SCAN_NB) {
-        hipLaunchKernelGGL(fpa_bwd_mid_kernel, head_grid((p.NB + NTHREADS / 64 - 1) / (NTHREADS / 64), p.H, p.BH),
-                           dim3(NTHREADS), 0, s, p);
+        const dim3 grid = head_grid((p.NB + NTHREADS / 64 - 1) / (NTHREADS / 64), p.H, p.BH);
+        if (p.NB <= MID_LDS_NB)
+            hipLaunchKernelGGL(fpa_bwd_mid_kernel<true>, grid, dim3(NTHREADS), 0, s, p);
+        else
+            hipLaunchKernelGGL(fpa_bwd_mid_kernel<false>, grid, dim3(NTHREADS), 0, s, p);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }

@@ -110,7 +110,8 @@ inline bool supported_d(int dtype, int D) {
     return D == 16 || D == 32 || D == 64 || D == 128 || D == 256;
 }
 
-// Most 64-blocks of T (the combine kernel stages three floats per block in LDS): T <= 524288.
-constexpr int MAX_NB = 8192;
+// Most 64-blocks of T: T <= 2097152.  The backward workspace holds 4 bytes per block pair (TBUF), 4 GiB
+// per head at this cap.
+constexpr int MAX_NB = 32768;
 
 }  // namespace fpa
