@@ -9,7 +9,7 @@ the key side writes (M the middle-block soft-min sum of a block pair),
 Below 160 blocks per head the combine adds that over every pair (stepping the pair index without a
 division, four pairs per thread at a time); from 160 blocks on a separate pass (one wave of 64 lanes
 per query block i) first turns row i into prefix sums Q_i(U), each relative to m_U = max(c_U ..
-c_{i-1}), and the combine adds sum_{i > U} 2^{c_U - max(c_U, max c over (U, i))} Q_i(U).  This file
+c_{i-1}), and stores them times 2^{c_U - m_U}, so that the combine adds sum_{i > U} of those.  This file
 restates both in float64 lane by lane as the kernels run them (the lane segments, the down pass
 with parked m_U, the affine-map scan across lanes, the up pass) and checks them against the direct
 sum, including rows shorter than a wave, rows that do not divide into 64 segments and a wide
@@ -70,7 +70,7 @@ def combine_pairs(c, V, U):
 
 
 def mid_pass(c, V):
-    """fpa_bwd_mid_kernel on one head: Q[U, i] = Q_i(U) in the upper triangle."""
+    """fpa_bwd_mid_kernel on one head: Q[U, i] = 2^{c_U - m_U} Q_i(U) in the upper triangle."""
     NB = len(c)
     Q = np.zeros((NB, NB))
     for i in range(2, NB):
@@ -100,16 +100,13 @@ def mid_pass(c, V):
             for U in range(lo, hi):
                 mn = Q[U + 1, i] if U + 1 < hi else mhi[l]
                 q = 2.0 ** (mn - m) * q + V[i, U]
-                Q[U + 1, i] = q
+                Q[U + 1, i] = 2.0 ** (c[U + 1] - mn) * q
                 m = mn
     return Q
 
 
 def combine_prefix(c, Q, U):
-    NB = len(c)
-    scanB = np.full(NB, -np.inf)                                   # max over (U, i]
-    scanB[U + 1:] = np.maximum.accumulate(c[U + 1:])
-    return sum(2.0 ** (c[U] - max(c[U], scanB[i - 1])) * Q[U, i] for i in range(U + 1, NB))
+    return sum(Q[U, i] for i in range(U + 1, len(c)))
 
 
 @pytest.mark.parametrize("NB,spread,seed", [(3, 1.0, 0), (9, 30.0, 1), (70, 5.0, 2), (131, 60.0, 3), (200, 20.0, 4)])
