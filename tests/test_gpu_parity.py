@@ -366,12 +366,14 @@ def test_large_scores(fpa):
     assert torch.isfinite(kern[4]).all() and errs["dphi"] <= 1e-2, ("dphi", errs["dphi"])
 
 
-def test_graph_replay_matches_eager(fpa):
+@pytest.mark.parametrize("T", [300, 700])
+def test_graph_replay_matches_eager(fpa, T):
     """The forward and backward captured in one HIP graph: three replays, with eager work and
     synchronisations between them, each give outputs bit-identical to the eager call (the
-    library records no memset nodes)."""
-    _say("[graph] B1 H2 T300 D64 fp16, capture and three replays")
-    q, k, v, phi, psi, beta, do = O.make_inputs(1, 2, 300, 64, dtype=torch.float16, seed=71)
+    library records no memset nodes).  At T = 700 the forward splits its heaviest row tiles and
+    runs its merge kernel on a workspace taken from the graph's pool."""
+    _say(f"[graph] B1 H2 T{T} D64 fp16, capture and three replays")
+    q, k, v, phi, psi, beta, do = O.make_inputs(1, 2, T, 64, dtype=torch.float16, seed=71)
     dev = "cuda"
     leaves = [t.to(dev).clone().requires_grad_() for t in (q, k, v, phi, psi, beta)]
     dod = do.to(dev)
