@@ -47,6 +47,12 @@ class FPADecoder(nn.Module):
         return self.head(self.ln(x))
 
     def loss(self, tokens):
-        """Next-token cross entropy of tokens (B, T + 1): inputs tokens[:, :-1], targets tokens[:, 1:]."""
+        """Next-token cross entropy of tokens (B, T + 1): inputs tokens[:, :-1], targets tokens[:, 1:].
+
+        The log-softmax reads the (fp16 under autocast) logits and works and writes in fp32 itself, so
+        no fp32 copy of the logits is made first (the same values as cross_entropy on logits.float());
+        autocast is off around it, since it would otherwise make that copy."""
         logits = self(tokens[:, :-1])
-        return F.cross_entropy(logits.float().reshape(-1, self.vocab), tokens[:, 1:].reshape(-1))
+        with torch.autocast(device_type=logits.device.type, enabled=False):
+            logp = torch.log_softmax(logits.reshape(-1, self.vocab), -1, dtype=torch.float32)
+            return F.nll_loss(logp, tokens[:, 1:].reshape(-1))
