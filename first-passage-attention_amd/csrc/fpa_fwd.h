@@ -35,9 +35,10 @@
 // Split the key range of the heaviest half of the row tiles when the launch's workgroups fill at most
 // this percentage of the slots (CUs x workgroups per CU); 0 never splits.  Measured on MI355X at
 // T = 2048, D = 64 fp16: at half the slots (B2 H12) the split forward with its merge takes 40 against
-// 47 us; at one or two full rounds (B4, B8 H12; B2 H8 T4096 fp32) it is 8-16% slower.
+// 47 us and at two thirds (B2 H16) 45.5 against 48.3; at three quarters (B3 H12) it is 6% slower, at
+// one or two full rounds (B4, B8 H12; B2 H8 T4096 fp32) 8-16% slower.
 #ifndef FPA_FWD_SPLIT_FILL
-#define FPA_FWD_SPLIT_FILL 50
+#define FPA_FWD_SPLIT_FILL 70
 #endif
 
 namespace fpa {

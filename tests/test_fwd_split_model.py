@@ -3,7 +3,7 @@
 fpa_fwd_kernel (csrc/fpa_fwd.h) takes its item from the workgroup id through xcd_work_item
 (csrc/fpa_common.h): a per-head item index k, 0 the heaviest.  With ns split row tiles per head
 (fwd_split_tiles in csrc/fpa_fwd.hip: half of the row tiles when the launch's workgroups fill at
-most half of the slots), items 3i and 3i + 1 are the two halves of the key range of row-tile rank i
+most 70% of the slots), items 3i and 3i + 1 are the two halves of the key range of row-tile rank i
 (part B: tiles jsplit .. jtmax, part A: tiles below jsplit) and item 3i + 2 is rank ns + i whole; the
 items after 3 ns are the remaining ranks.  This file emulates that index arithmetic and checks, over
 shapes with and without heads in multiples of 8 and ragged T, that every row tile is covered exactly
@@ -21,7 +21,7 @@ sys.path.insert(0, os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(
 
 NW, BM, BN, G = 4, 128, 64, 64
 XCD_CUS, CUS = 32, 256
-FILL = 50                            # FPA_FWD_SPLIT_FILL
+FILL = 70                            # FPA_FWD_SPLIT_FILL
 WPE16, WPE32 = 3, 2                  # FPA_FWD_WPE, FPA_FWD_WPE32
 
 
@@ -120,6 +120,8 @@ def test_workspace_bytes_match_the_split(B, H, T, dtype, D):
 
 def test_split_only_where_the_launch_is_short():
     assert split_tiles(24, 2048, 0, 64) == 8        # B2 H12: 384 workgroups, 768 slots
+    assert split_tiles(32, 2048, 0, 64) == 8        # B2 H16: 512 workgroups
+    assert split_tiles(36, 2048, 0, 64) == 0        # B3 H12: 576 workgroups
     assert split_tiles(48, 2048, 0, 64) == 0        # cfg2: 768 workgroups
     assert split_tiles(16, 4096, 1, 128) == 0       # cfg3: 512 workgroups, 256 slots
     assert split_tiles(12, 16381, 0, 64) == 0       # cfg4
