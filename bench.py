@@ -158,10 +158,10 @@ BWD_KERNELS = (("fpa_bwd_prep", 1, 0), ("fpa_bwd_kvq_kernel", 2 | 4, 10), ("fpa_
 LM = dict(B=8, T=2048, d_model=768, n_heads=12, layers=12, d_mlp=3072, vocab=32000)
 
 
-def lm_step_ms(steps, warmup):
+def lm_step_ms(steps, warmup, fb=True):
     """cfg5: ms per training step of the LM (see the module docstring), the last loss, ms of the
-    forward+backward alone (BASELINE.json's cfg5: one forward+backward, no optimizer step) and the
-    optimizer used."""
+    forward+backward alone (BASELINE.json's cfg5: one forward+backward, no optimizer step; None when
+    fb is False) and the optimizer used."""
     import torch
     from fpa.lm import FPADecoder
 
@@ -201,7 +201,7 @@ def lm_step_ms(steps, warmup):
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / steps
     loss = loss.item()
-    fb_ms = time_steps(fwd_bwd, steps, warmup)
+    fb_ms = time_steps(fwd_bwd, steps, warmup) if fb else None
     del model, opt
     torch.cuda.empty_cache()
     return ms, loss, fb_ms, opt_name
@@ -211,7 +211,7 @@ def run_lm(a):
     """--workload lm: the cfg5 training step as the bench line."""
     import torch
     torch.cuda.set_device(0)
-    ms, loss, fb_ms, opt_name = lm_step_ms(a.steps, a.warmup)
+    ms, loss, fb_ms, opt_name = lm_step_ms(a.steps, a.warmup, fb=not a.no_extra)
     ntok = LM["B"] * LM["T"]
     res = {
         "metric": "LM training step tokens/s (cfg5: 12-layer d768 H12 FPA decoder, B8 T2048, fp16 autocast)",
@@ -226,8 +226,8 @@ def run_lm(a):
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic (uniform random tokens, random-init weights)",
-        "fwd_bwd_ms": round(fb_ms, 3),
-        "fwd_bwd_tokens_per_s": round(ntok / (fb_ms * 1e-3), 1),
+        "fwd_bwd_ms": round(fb_ms, 3) if fb_ms else None,
+        "fwd_bwd_tokens_per_s": round(ntok / (fb_ms * 1e-3), 1) if fb_ms else None,
         "config": {"workload": f"cfg5: FPADecoder training step ({opt_name}, grad scaler)", **LM,
                    "parallelism": "single GPU"},
         "final_loss": round(loss, 4),
@@ -351,7 +351,8 @@ def main():
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline legs")
-    ap.add_argument("--no-extra", action="store_true", help="skip the other configs (cfg3, cfg4, cfg5)")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the other configs (cfg3, cfg4, cfg5); with --workload lm, the forward+backward timing")
     ap.add_argument("--shape", help="B,H,T,D: time this shape instead of --config (the config's distributions)")
     ap.add_argument("--dtype", choices=("fp16", "fp32"), default=None, help="with --shape (default fp16)")
     ap.add_argument("--rounds", type=int, default=5, help="rounds of the reference's timing protocol")
