@@ -27,10 +27,13 @@ int64_t tp_of(int64_t T) { return ((T + G - 1) / G) * G; }
 int64_t align64(int64_t n) { return (n + 63) / 64 * 64; }  // floats -> 256-byte multiple
 
 struct WsLayout {
-    int64_t qinfo, wsum, rsum, gd, tbuf, dbp, total;  // float offsets
+    int64_t qinfo, wsum, rsum, gd, tbuf, dbp, pkv, pks, pq, pqr, total;  // float offsets
+    int64_t KS, QS;  // split keys < KS and queries >= QS (KS = 0, QS = T: no split)
 };
 
-WsLayout ws_layout(int64_t B, int64_t H, int64_t T) {
+// The split-tile regions are sized for the launch that runs both backward sides as one (the fused
+// launch splits its heaviest tiles when it fills few of the GPU's slots).
+WsLayout ws_layout(int64_t B, int64_t H, int64_t T, int64_t D, int32_t dtype) {
     const int64_t BH = B * H, TP = tp_of(T), NB = TP / G, NK32 = (T + 31) / 32;
     WsLayout w;
     int64_t off = 0;
@@ -39,7 +42,16 @@ WsLayout ws_layout(int64_t B, int64_t H, int64_t T) {
     w.rsum = off;  off += align64(BH * TP);
     w.gd = off;    off += align64(BH * NB * G * G);
     w.tbuf = off;  off += align64(BH * NB * NB);
-    w.dbp = off;   off += align64(BH * NK32);
+    w.dbp = off;   off += align64(2 * BH * NK32);
+    int nks = 0, nqs = 0;
+    if ((dtype == FPA_F16 || dtype == FPA_F32) && supported_d(dtype, (int)D)) bwd_split_tiles(BH, T, dtype, (int)D, nks, nqs);
+    const int64_t BT = 32 * FPA_NW, nt = (T + BT - 1) / BT;
+    w.KS = nks * BT;
+    w.QS = nqs ? (nt - nqs) * BT : T;
+    w.pkv = off;   off += align64(2 * BH * w.KS * 2 * D);
+    w.pks = off;   off += align64(2 * BH * w.KS * 2);
+    w.pq = off;    off += align64(2 * BH * (T - w.QS) * D);
+    w.pqr = off;   off += align64(2 * BH * (T - w.QS));
     w.total = off;
     return w;
 }
@@ -155,9 +167,7 @@ int64_t fpa_fwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D, int3
 }
 
 int64_t fpa_bwd_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D, int32_t dtype) {
-    (void)D;
-    (void)dtype;
-    return ws_layout(B, H, T).total * (int64_t)sizeof(float);
+    return ws_layout(B, H, T, D, dtype).total * (int64_t)sizeof(float);
 }
 
 int64_t fpa_field_workspace_bytes(int64_t B, int64_t T, int64_t C, int64_t H) {
@@ -272,7 +282,7 @@ int bwd_impl(const FpaBwdArgs *a, void *wsp, void *stream) {
         return fail(FPA_ERR_INVALID, "beta, lse, state, dphi, dpsi and dbeta must be non-NULL");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int64_t TP = tp_of(a->T);
-    const WsLayout wl = ws_layout(a->B, a->H, a->T);
+    const WsLayout wl = ws_layout(a->B, a->H, a->T, a->D, a->dtype);
     float *ws = static_cast<float *>(wsp);
     BwdParams p;
     p.q = a->q; p.sq = s3(a->sq);
@@ -288,17 +298,24 @@ int bwd_impl(const FpaBwdArgs *a, void *wsp, void *stream) {
     p.qinfo = ws + wl.qinfo;
     p.wsum = ws + wl.wsum; p.rsum = ws + wl.rsum;
     p.gd = ws + wl.gd; p.tbuf = ws + wl.tbuf; p.dbp = ws + wl.dbp;
+    p.pkv = ws + wl.pkv; p.pks = ws + wl.pks; p.pq = ws + wl.pq; p.pqr = ws + wl.pqr;
     p.B = (int)a->B; p.H = (int)a->H; p.T = (int)a->T; p.TP = (int)TP; p.NB = (int)(TP / G);
     p.BH = (int)(a->B * a->H); p.NK32 = (int)((a->T + 31) / 32);
     p.sc2 = LOG2E / sqrtf((float)a->D);
     p.smscale = 1.0f / sqrtf((float)a->D);
     p.il2 = LOG2E / a->tau;
     const int ph = a->phases ? a->phases : 31;
+    // The split tiles run only in the launch of both sides together; their merge follows it.
+    const bool both = (ph & FPA_BWD_KEYS) && (ph & FPA_BWD_QUERIES);
+    p.KS = both ? (int)wl.KS : 0;
+    p.QS = both ? (int)wl.QS : p.T;
     hipError_t e;
     if ((ph & FPA_BWD_DELTA) && (e = launch_bwd_prep(p, a->dtype, (int)a->D, s)) != hipSuccess)
         return hip_fail(e, "fpa_bwd_prep launch");
-    if ((ph & FPA_BWD_KEYS) && (ph & FPA_BWD_QUERIES)) {
+    if (both) {
         if ((e = launch_bwd_kvq(p, a->dtype, (int)a->D, s)) != hipSuccess) return hip_fail(e, "fpa_bwd_kvq launch");
+        if (p.KS > 0 && (e = launch_bwd_merge(p, a->dtype, (int)a->D, s)) != hipSuccess)
+            return hip_fail(e, "fpa_bwd_merge launch");
     } else {
         if ((ph & FPA_BWD_KEYS) && (e = launch_bwd_kv(p, a->dtype, (int)a->D, s)) != hipSuccess)
             return hip_fail(e, "fpa_bwd_kv launch");
@@ -362,7 +379,7 @@ int fpa_bwd_noalloc(const FpaBwdArgs *a, void *stream) {
     if (a == nullptr) return fail(FPA_ERR_INVALID, "args is NULL");
     int rc = check_common(a->B, a->H, a->T, a->D, a->dtype, a->tau);
     if (rc) return rc;
-    const int64_t need = ws_layout(a->B, a->H, a->T).total * (int64_t)sizeof(float);
+    const int64_t need = ws_layout(a->B, a->H, a->T, a->D, a->dtype).total * (int64_t)sizeof(float);
     if (need > FPA_NOALLOC_SCRATCH_BYTES)
         return fail(FPA_ERR_UNSUPPORTED, "fpa_bwd_noalloc: this problem needs " + std::to_string(need) +
                                              " bytes of scratch, more than the " +

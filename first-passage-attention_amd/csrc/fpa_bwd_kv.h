@@ -71,9 +71,12 @@ struct KvShared {
 };
 
 // Keys [32 NW kt, 32 NW (kt + 1)) of head bh: every query block from the keys' diagonal block to T.
-template <typename T, int D, int NW>
+// SPLIT (small fused launches): half 1 takes the query blocks from the diagonal one up to ibs =
+// ib0 + max(2, (NB - ib0) / 2) (both diagonal blocks of the tile), half 2 the blocks from ibs on; each
+// writes its sums to the split-tile partials (pkv, pks, the second half of dbp) for the merge kernel.
+template <typename T, int D, int NW, bool SPLIT = false>
 __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, NW> &sm, const int kt, const int bh,
-                                            const int part = 0) {
+                                            const int part = 0, const int half = 0) {
     constexpr int BK = 32 * NW, BQ = 64;   // keys per workgroup, queries per iteration (one block)
     constexpr int DT = D < 32 ? 32 : D;
     constexpr int NDT = DT / 32 / kv_parts<T, D>();  // dK / dV column tiles of this part
@@ -116,7 +119,17 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
             buf_lds16(buf_rsrc(qi_head + (int64_t)ib * QI_PLANES * 64), 1024 * hq + 16 * lane, aI + buf * sizeof(qi[0]) + 1024 * hq);
     };
     const int ib0 = k0 / G;
-    issue(ib0, 0);
+    int iblo = ib0, ibhi = p.NB;
+    if constexpr (SPLIT) {
+        if (half != 0) {
+            const int ibs = ib0 + max(2, (p.NB - ib0) / 2);
+            if (half == 1)
+                ibhi = ibs;
+            else
+                iblo = ibs;
+        }
+    }
+    issue(iblo, 0);
 
     OpRow<T, D> kreg, vreg;
     load_row_p1<T, D>(kreg, Kb + (int64_t)s * p.sk.t, s_valid, g);
@@ -168,6 +181,24 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
     // current query block.  After a block the middle takes in its BMIN / BLSE (staged with the
     // block's per-query values) and both are recomputed for the next block, before its barrier.
     float rs = Cs, sv = (Cs > ninf()) ? fexp2(sufl - Cs) : 0.f;
+    if constexpr (SPLIT) {
+        if (half == 2 && wave_active) {  // blocks jb + 1 .. iblo - 1 are between the keys and the first query block
+            const float *bmin = p.state + L.bplane(BP_MIN) + brow, *blse = p.state + L.bplane(BP_LSE) + brow;
+            float m = pinf(), l = ninf();
+            for (int j0 = jb + 1; j0 < iblo; j0 += 64) {
+                const int j = j0 + lane;
+                if (j < iblo) {
+                    m = fminf(m, bmin[j]);
+                    l = lse2_pair(l, blse[j]);
+                }
+            }
+            mid = wave_min(m);
+            midl = wave_reduce(l, [](float a, float b) { return lse2_pair(a, b); });
+            cmid = (mid < pinf()) ? -mid * p.il2 : ninf();
+            rs = fmaxf(Cs, cmid);
+            sv = (rs > ninf()) ? fexp2(sufl - rs) + fexp2(midl - rs) : 0.f;
+        }
+    }
     wait_loads();
     __syncthreads();
     constexpr int NS = KvShared<T, D, NW>::NS;
@@ -179,7 +210,7 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
         if ((w & 1) == 0 && lane == 0 && scalars && wave_active && ibp > jb + 1)
             p.tbuf[(brow + ibp) * p.NB + jb] = sm.tpx[par][w] + sm.tpx[par][w + 1];
     };
-    for (int ib = ib0, it = 0; ib < p.NB; ++ib, ++it) {
+    for (int ib = iblo, it = 0; ib < ibhi; ++ib, ++it) {
         const int buf = (NS == 2) ? (it & 1) : 0;
         if constexpr (NS == 2) issue(umin_i(ib + 1, p.NB - 1), buf ^ 1);
         if (it > 0) flush_tbuf(ib - 1, (it - 1) & 1);
@@ -378,12 +409,34 @@ __device__ __forceinline__ void bwd_kv_tile(const BwdParams &p, KvShared<T, D, N
         __syncthreads();
     }
 
-    flush_tbuf(p.NB - 1, (p.NB - 1 - ib0) & 1);
+    flush_tbuf(ibhi - 1, (ibhi - 1 - iblo) & 1);
     // Per-key outputs (lanes c and c + 32 hold the same key, different queries).
     gsum = sum_halves(gsum);
     Wacc = sum_halves(Wacc);
     const float dbw = XB ? wave_sum(dbacc) : wave_sum(dbacc) / beff;
     if (!wave_active) return;
+    if constexpr (SPLIT) {
+        if (half != 0) {  // partial sums of a split tile (keys < KS < T): raw dK / dV accumulators
+            const int hp = half - 1;
+            if (lane == 0) p.dbp[((int64_t)hp * p.BH + bh) * p.NK32 + kw0 / 32] = dbw;
+            const int64_t ks = ((int64_t)hp * p.BH + bh) * p.KS + s;
+            if (g == 0) *reinterpret_cast<f32x2 *>(p.pks + 2 * ks) = f32x2{Wacc, gsum};
+            float *row = p.pkv + ks * 2 * D;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                for (int jq = 0; jq < 4; ++jq) {
+                    const int d0 = 32 * (dt0 + dt) + 8 * jq + 4 * g;
+                    if (d0 < D) {
+                        *reinterpret_cast<f32x4 *>(row + d0) = f32x4{dkacc[dt][4 * jq + 0], dkacc[dt][4 * jq + 1],
+                                                                     dkacc[dt][4 * jq + 2], dkacc[dt][4 * jq + 3]};
+                        *reinterpret_cast<f32x4 *>(row + D + d0) = f32x4{dvacc[dt][4 * jq + 0], dvacc[dt][4 * jq + 1],
+                                                                         dvacc[dt][4 * jq + 2], dvacc[dt][4 * jq + 3]};
+                    }
+                }
+            return;
+        }
+    }
     if (scalars) {
         if (lane == 0) p.dbp[(int64_t)bh * p.NK32 + kw0 / 32] = dbw;  // one partial per 32-key group
         if (g == 0 && s < p.TP) p.wsum[rowbase + s] = Wacc;

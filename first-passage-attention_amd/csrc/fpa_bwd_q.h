@@ -54,8 +54,12 @@ struct QShared {
 };
 
 // Queries [32 NW qt, 32 NW (qt + 1)) of head bh: every key block from their diagonal block down to 0.
-template <typename T, int D, int NW>
-__device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW> &sm, const int qt, const int bh) {
+// SPLIT (small fused launches): half 1 takes the key blocks from jbmax down to jbs = jbmax + 1 -
+// max(2, (jbmax + 1) / 2) (both diagonal blocks of the tile), half 2 the blocks below jbs; each writes
+// its dQ accumulators and R to the split-tile partials (pq, pqr) for the merge kernel.
+template <typename T, int D, int NW, bool SPLIT = false>
+__device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW> &sm, const int qt, const int bh,
+                                           const int half = 0) {
     constexpr int BM = 32 * NW, BK = 64;  // queries per workgroup, keys per iteration (one block)
     constexpr int DT = D < 32 ? 32 : D;
     constexpr int NDT = DT / 32;
@@ -100,7 +104,17 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
             buf_lds16(buf_rsrc(st_head + jb * BK), hq ? bst_off : kst_off, aS + buf * sizeof(kst[0]) + 1024 * hq);
     };
     const int jbmax = umin_i(p.NB - 1, (q0 + BM - 1) / BK);
-    issue(jbmax, 0);
+    int jbhi = jbmax, jblo = 0;
+    if constexpr (SPLIT) {
+        if (half != 0) {
+            const int jbs = jbmax + 1 - max(2, (jbmax + 1) / 2);
+            if (half == 1)
+                jblo = jbs;
+            else
+                jbhi = jbs - 1;
+        }
+    }
+    issue(jbhi, 0);
 
     OpRow<T, D> qreg, doreg;
     load_row_p1<T, D>(qreg, Qb + (int64_t)tq * p.sq.t, t_valid, g);
@@ -144,10 +158,29 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
 
     // BMIN / BLSE of block jb + 1 (which joins the middle), from the previous block's staged values.
     float bm_prev = 0.f, bl_prev = 0.f;
+    if constexpr (SPLIT) {
+        if (half == 2 && wave_active) {  // blocks jbs + 1 .. ib - 1 are between; block jbs joins them first
+            const int jbs = jbhi + 1;
+            const float *bmin = p.state + L.bplane(BP_MIN) + brow, *blse = p.state + L.bplane(BP_LSE) + brow;
+            float m = pinf(), l = ninf();
+            for (int j0 = jbs + 1; j0 < ib; j0 += 64) {
+                const int j = j0 + lane;
+                if (j < ib) {
+                    m = fminf(m, bmin[j]);
+                    l = lse2_pair(l, blse[j]);
+                }
+            }
+            mid = wave_min(m);
+            midl = wave_reduce(l, [](float a, float b) { return lse2_pair(a, b); });
+            cmid = (mid < pinf()) ? -mid * p.il2 : ninf();
+            bm_prev = ld_uniform(bmin, jbs);
+            bl_prev = ld_uniform(blse, jbs);
+        }
+    }
     wait_loads();
     __syncthreads();
     constexpr int NS = QShared<T, D, NW>::NS;
-    for (int jb = jbmax, it = 0; jb >= 0; --jb, ++it) {
+    for (int jb = jbhi, it = 0; jb >= jblo; --jb, ++it) {
         const int buf = (NS == 2) ? (it & 1) : 0;
         const int s0 = jb * BK;
         if constexpr (NS == 2) issue(jb > 0 ? jb - 1 : 0, buf ^ 1);
@@ -334,6 +367,24 @@ __device__ __forceinline__ void bwd_q_tile(const BwdParams &p, QShared<T, D, NW>
 
     racc = sum_halves(racc);
     if (!wave_active) return;
+    if constexpr (SPLIT) {
+        if (half != 0) {  // partial sums of a split tile (queries QS .. T - 1): raw dQ accumulators and R
+            if (!t_valid) return;
+            const int64_t qs = ((int64_t)(half - 1) * p.BH + bh) * (p.T - p.QS) + (tq - p.QS);
+            if (g == 0) p.pqr[qs] = racc;
+            float *row = p.pq + qs * D;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                for (int jq = 0; jq < 4; ++jq) {
+                    const int d0 = 32 * dt + 8 * jq + 4 * g;
+                    if (d0 < D)
+                        *reinterpret_cast<f32x4 *>(row + d0) = f32x4{dqacc[dt][4 * jq + 0], dqacc[dt][4 * jq + 1],
+                                                                     dqacc[dt][4 * jq + 2], dqacc[dt][4 * jq + 3]};
+                }
+            return;
+        }
+    }
     if (g == 0 && tq < p.TP) p.rsum[rowbase + tq] = t_valid ? racc : 0.f;
     if (!t_valid) return;
     T *dQr = static_cast<T *>(p.dq) + b * p.sdq.b + h * p.sdq.h + (int64_t)tq * p.sdq.t;

@@ -59,7 +59,15 @@ struct BwdParams {
     float *rsum;   // BH * TP   query-block soft-min sums R_t
     float *gd;     // BH * NB * G * G   gated dS of in-block pairs, [s][t]
     float *tbuf;   // BH * NB * NB      middle-block sums
-    float *dbp;    // BH * NK32         dbeta partials, one per 32-key group
+    float *dbp;    // 2 * BH * NK32     dbeta partials, one per 32-key group (the second half: far parts)
+    // Split tiles (small fused launches): the nks heaviest key tiles (keys < KS = 128 nks) and the nqs
+    // heaviest query tiles (queries >= QS) run as two items each over halves of their block range
+    // (near: the diagonal side), writing partial results that the combine adds.  KS = 0 and QS = T: none.
+    float *pkv;    // 2 * BH * KS * 2D  dK and dV accumulators per part and key
+    float *pks;    // 2 * BH * KS * 2   W and the gated dS sum per part and key
+    float *pq;     // 2 * BH * (T - QS) * D  dQ accumulators per part and query
+    float *pqr;    // 2 * BH * (T - QS)      R per part and query
+    int KS, QS;
     int B, H, T, TP, NB, BH, NK32;
     float sc2;     // log2(e) / sqrt(D)
     float smscale; // 1 / sqrt(D)
@@ -101,6 +109,10 @@ hipError_t launch_bwd_kv(const BwdParams &p, int dtype, int D, hipStream_t s);
 hipError_t launch_bwd_q(const BwdParams &p, int dtype, int D, hipStream_t s);
 hipError_t launch_bwd_kvq(const BwdParams &p, int dtype, int D, hipStream_t s);  // both sides, one launch
 hipError_t launch_bwd_combine(const BwdParams &p, hipStream_t s);
+// Adds the two parts of the split tiles (before the combine): dk, dv, dpsi, W, dq, R, dbeta partials.
+hipError_t launch_bwd_merge(const BwdParams &p, int dtype, int D, hipStream_t s);
+// Key and query tiles per head that the fused backward splits (0, 0: none) for a (BH, T) problem.
+void bwd_split_tiles(int64_t BH, int64_t T, int dtype, int D, int &nks, int &nqs);
 hipError_t launch_field_fwd(const FieldParams &p, int dtype, hipStream_t s);
 hipError_t launch_field_bwd(const FieldParams &p, int dtype, hipStream_t s);
 

@@ -110,29 +110,82 @@ def test_kernel_deterministic(fpa):
         assert all(torch.equal(x, y) for x, y in zip(*runs))
 
 
+def _unsplit_ws_bytes(B, H, T):
+    """Backward workspace bytes of a shape whose fused launch splits no tile."""
+    a64 = lambda n: (n + 63) // 64 * 64  # noqa: E731
+    BH, TP = B * H, (T + 63) // 64 * 64
+    NB, NK32 = TP // 64, (T + 31) // 32
+    return 4 * (a64(8 * BH * TP) + 2 * a64(BH * TP) + a64(BH * NB * 4096) + a64(BH * NB * NB) + a64(2 * BH * NK32))
+
+
+def _bwd_runs(q, k, v, phi, psi, beta, do, phase_sets):
+    """dq, dk, dv, dphi, dpsi, dbeta of the HIP backward run once per set of fpa_bwd phases."""
+    from fpa import _hip
+    dev = torch.device("cuda")
+    fb = _hip.FwdBuffers(q)
+    _hip.run_fwd(_hip.fwd_args(q, k, v, phi, psi, beta, 1.0, fb), dev)
+    gb = _hip.BwdBuffers(q)
+    ba = _hip.bwd_args(q, k, v, beta, 1.0, fb, do, gb)
+    outs = []
+    for phases in phase_sets:
+        for ph in phases:
+            ba.phases = ph
+            _hip.run_bwd(ba, dev)
+        torch.cuda.synchronize()
+        outs.append([t.clone() for t in (gb.dq, gb.dk, gb.dv, gb.dphi, gb.dpsi, gb.dbeta)])
+    return outs
+
+
 def test_fused_backward_matches_separate_launches(fpa):
     """The backward's key and query sides run as one launch; launched one by one through the
     phases bitmask they give bit-identical gradients (head counts with and without the per-XCD
-    head placement, a ragged T, and fp32 D128)."""
+    head placement, a ragged T, and fp32 D128; shapes whose fused launch does not split tiles)."""
     from fpa import _hip, _lib
     dev = torch.device("cuda")
-    for (B, H, T, D, dtype), seed in (((2, 4, 600, 64, torch.float16), 14), ((1, 3, 333, 64, torch.float16), 15),
+    for (B, H, T, D, dtype), seed in (((2, 4, 300, 64, torch.float16), 14), ((1, 3, 333, 64, torch.float16), 15),
                                       ((1, 2, 260, 128, torch.float32), 16), ((1, 2, 200, 64, torch.float32), 17)):
         _say(f"[fused] B{B} H{H} T{T} D{D} {dtype}")
         q, k, v, phi, psi, beta, do = (t.to(dev) for t in O.make_inputs(B, H, T, D, dtype=dtype, seed=seed))
-        fb = _hip.FwdBuffers(q)
-        _hip.run_fwd(_hip.fwd_args(q, k, v, phi, psi, beta, 1.0, fb), dev)
-        gb = _hip.BwdBuffers(q)
-        ba = _hip.bwd_args(q, k, v, beta, 1.0, fb, do, gb)
-        outs = []
-        for phases in ((0,), (_lib.FPA_BWD_DELTA, _lib.FPA_BWD_KEYS, _lib.FPA_BWD_QUERIES,
-                              _lib.FPA_BWD_PHI | _lib.FPA_BWD_BETA)):
-            for ph in phases:
-                ba.phases = ph
-                _hip.run_bwd(ba, dev)
-            torch.cuda.synchronize()
-            outs.append([t.clone() for t in (gb.dq, gb.dk, gb.dv, gb.dphi, gb.dpsi, gb.dbeta)])
+        assert _hip._bwd_ws_bytes(B, H, T, D, _lib.dtype_code(dtype)) == _unsplit_ws_bytes(B, H, T)
+        outs = _bwd_runs(q, k, v, phi, psi, beta, do, ((0,), (_lib.FPA_BWD_DELTA, _lib.FPA_BWD_KEYS,
+                                                                _lib.FPA_BWD_QUERIES, _lib.FPA_BWD_PHI | _lib.FPA_BWD_BETA)))
         assert all(torch.equal(x, y) for x, y in zip(*outs))
+
+
+BWD_SPLIT_CASES = [  # (B, H, T, D, dtype, beta, seed): shapes whose fused backward splits its heaviest tiles
+    (2, 4, 600, 64, torch.float16, None, 51),                  # B*H = 8: heads pinned to XCDs
+    (1, 3, 1000, 32, torch.float16, (-0.7, 0.0, 1.3), 52),
+    (1, 2, 777, 32, torch.float32, None, 53),
+    (1, 1, 4100, 128, torch.float16, None, 54),
+    (1, 1, 513, 16, torch.float16, None, 55),
+    (1, 4, 4096, 64, torch.float16, None, 56),
+]
+
+
+@pytest.mark.parametrize("B,H,T,D,dtype,beta,seed", BWD_SPLIT_CASES)
+def test_split_backward(fpa, B, H, T, D, dtype, beta, seed):
+    """When the fused backward fills at most 70% of the slots, the heaviest half of its key tiles and of
+    its query tiles run as two items each over halves of their block range, and a merge kernel adds the
+    partial sums before the combine.  Launched one side at a time (phases), the backward runs every tile
+    whole: the gradients agree to rounding.  Through the split path the gradients agree with the oracle
+    (for fp16 the oracle fed the kernel's own stored output, as in test_split_forward)."""
+    from fpa import _hip, _lib
+    _say(f"[bwd split] B{B} H{H} T{T} D{D} {dtype}")
+    q, k, v, phi, psi, b0, do = O.make_inputs(B, H, T, D, dtype=dtype, seed=seed, psi_noise=1.0)
+    beta = torch.tensor(beta) if beta is not None else b0
+    dev = torch.device("cuda")
+    assert _hip._bwd_ws_bytes(B, H, T, D, _lib.dtype_code(dtype)) > _unsplit_ws_bytes(B, H, T)
+    qd, kd, vd, pd, sd, bd, dod = (t.to(dev) for t in (q, k, v, phi, psi, beta, do))
+    split, whole = _bwd_runs(qd, kd, vd, pd, sd, bd, dod, ((0,), (_lib.FPA_BWD_DELTA, _lib.FPA_BWD_KEYS,
+                                                                 _lib.FPA_BWD_QUERIES, _lib.FPA_BWD_PHI)))
+    tol = 1e-3 if dtype == torch.float16 else 1e-5
+    for name, x, y in zip(NAMES[1:], split, whole):
+        assert O.rel_err(x.cpu(), y.cpu()) <= (1e-2 if name == "dbeta" and dtype == torch.float16 else tol), name
+    kern = run_hip(fpa, q, k, v, phi, psi, beta, do)
+    ref = O.fpa_grads_chunked(q, k, v, phi, psi, beta, do, device="cuda")
+    if dtype == torch.float16:
+        ref = ref[:1] + list(O.fpa_grads_stored(q, k, v, phi, psi, beta, do, o_stored=kern[0])[1:])
+    check(kern, ref, dtype)
 
 
 SPLIT_CASES = [  # (B, H, T, D, dtype, beta, seed): shapes whose forward splits its heaviest row tiles

@@ -1,8 +1,9 @@
 """fpa_bwd_noalloc: the backward on the library's static scratch gives fpa_bwd's results.
 
-Two calls in a row through the C ABI, the second with a smaller problem (the scratch keeps the
-first call's contents), each compared bit for bit with fpa_bwd on a torch-allocated workspace;
-a problem whose scratch need exceeds the static array is refused before any launch.
+Three calls in a row through the C ABI, each with a smaller problem than the one before (the scratch
+keeps the previous call's contents; the first call's fused launch splits its heaviest tiles and adds
+their halves through the scratch), each compared bit for bit with fpa_bwd on a torch-allocated
+workspace; a problem whose scratch need exceeds the static array is refused before any launch.
 """
 import sys
 
@@ -42,7 +43,8 @@ def _both(B, H, T, D, dtype, seed):
 def test_noalloc_backward_matches_fpa_bwd():
     if not torch.cuda.is_available():
         pytest.skip("needs a GPU")
-    for (B, H, T, D, dtype), seed in (((2, 3, 300, 64, torch.float16), 91), ((1, 2, 100, 32, torch.float32), 92)):
+    for (B, H, T, D, dtype), seed in (((1, 3, 1000, 32, torch.float16), 90), ((2, 3, 300, 64, torch.float16), 91),
+                                      ((1, 2, 100, 32, torch.float32), 92)):
         _say(f"[noalloc] B{B} H{H} T{T} D{D} {dtype}")
         (with_ws, noalloc), ref = _both(B, H, T, D, dtype, seed)
         for name, x, y in zip(("dq", "dk", "dv", "dphi", "dpsi", "dbeta"), with_ws, noalloc):
