@@ -23,8 +23,10 @@
 #endif
 // Split the heaviest half of the key tiles and of the query tiles (two items each over halves of their
 // block range) when the fused launch fills at most this percentage of the slots; 0 never splits.
+// Measured at D = 64 fp16: 75% of the slots (B1 H12 T2048) 81 -> 59 us, 100% (B2 H8 T2048) 80.7 -> 79.0,
+// 150% (B2 H12 T2048) 86 -> 102.
 #ifndef FPA_BWD_SPLIT_FILL
-#define FPA_BWD_SPLIT_FILL 70
+#define FPA_BWD_SPLIT_FILL 100
 #endif
 
 namespace fpa {

@@ -1,6 +1,6 @@
 """The backward's split tiles, restated on the CPU.
 
-When the fused backward (both sides in one launch) fills at most 70% of the GPU's slots
+When the fused backward (both sides in one launch) fills at most all of the GPU's slots
 (bwd_split_tiles in csrc/fpa_bwd_fused.hip), the heaviest half of the key tiles and of the query tiles
 run as two items each: a key tile's query blocks from its diagonal block ib0 up to ibs = ib0 + max(2,
 (NB - ib0) / 2) and from ibs on; a query tile's key blocks from jbmax down to jbs = jbmax + 1 - max(2,
@@ -18,7 +18,7 @@ import pytest
 sys.path.insert(0, os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "first-passage-attention_amd"))
 
 NW, BT, G = 4, 128, 64
-CUS, FILL, FUSED_MAX = 256, 70, 1024
+CUS, FILL, FUSED_MAX = 256, 100, 1024
 
 
 def kv_wpe(dtype, D):
@@ -105,7 +105,9 @@ def test_workspace_bytes_hold_the_partials(B, H, T, dtype, D):
 
 
 def test_split_only_where_the_launch_is_short():
-    assert split_tiles(12, 2048, 0, 64) == (0, 0)    # B1 H12 T2048: 384 items, 75% of the 512 slots
+    assert split_tiles(12, 2048, 0, 64) == (8, 8)    # B1 H12 T2048: 384 items, 75% of the 512 slots
+    assert split_tiles(16, 2048, 0, 64) == (8, 8)    # B1 H16: 512 items, all of them
+    assert split_tiles(24, 2048, 0, 64) == (0, 0)    # B2 H12: 768 items
     assert split_tiles(8, 2048, 0, 64) == (8, 8)     # B1 H8: 256 items
     assert split_tiles(4, 4096, 0, 64) == (16, 16)
     assert split_tiles(48, 2048, 0, 64) == (0, 0)    # cfg2

@@ -164,7 +164,7 @@ BWD_SPLIT_CASES = [  # (B, H, T, D, dtype, beta, seed): shapes whose fused backw
 
 @pytest.mark.parametrize("B,H,T,D,dtype,beta,seed", BWD_SPLIT_CASES)
 def test_split_backward(fpa, B, H, T, D, dtype, beta, seed):
-    """When the fused backward fills at most 70% of the slots, the heaviest half of its key tiles and of
+    """When the fused backward fills at most all of the slots, the heaviest half of its key tiles and of
     its query tiles run as two items each over halves of their block range, and a merge kernel adds the
     partial sums before the combine.  Launched one side at a time (phases), the backward runs every tile
     whole: the gradients agree to rounding.  Through the split path the gradients agree with the oracle
