@@ -33,7 +33,7 @@ struct WsLayout {
 
 // The split-tile regions are sized for the launch that runs both backward sides as one (the fused
 // launch splits its heaviest tiles when it fills few of the GPU's slots).
-WsLayout ws_layout(int64_t B, int64_t H, int64_t T, int64_t D, int32_t dtype) {
+WsLayout ws_layout(int64_t B, int64_t H, int64_t T, int64_t D, int32_t dtype, bool split_ok = true) {
     const int64_t BH = B * H, TP = tp_of(T), NB = TP / G, NK32 = (T + 31) / 32;
     WsLayout w;
     int64_t off = 0;
@@ -44,7 +44,8 @@ WsLayout ws_layout(int64_t B, int64_t H, int64_t T, int64_t D, int32_t dtype) {
     w.tbuf = off;  off += align64(BH * NB * NB);
     w.dbp = off;   off += align64(2 * BH * NK32);
     int nks = 0, nqs = 0;
-    if ((dtype == FPA_F16 || dtype == FPA_F32) && supported_d(dtype, (int)D)) bwd_split_tiles(BH, T, dtype, (int)D, nks, nqs);
+    if (split_ok && (dtype == FPA_F16 || dtype == FPA_F32) && supported_d(dtype, (int)D))
+        bwd_split_tiles(BH, T, dtype, (int)D, nks, nqs);
     const int64_t BT = 32 * FPA_NW, nt = (T + BT - 1) / BT;
     w.KS = nks * BT;
     w.QS = nqs ? (nt - nqs) * BT : T;
@@ -266,8 +267,9 @@ int fpa_fwd(const FpaFwdArgs *a, void *stream) {
 namespace {
 
 // The backward of fpa_bwd and fpa_bwd_noalloc: every check but the workspace's, then the launches
-// with their scratch regions carved out of `wsp` (fpa_bwd_workspace_bytes bytes, 256-byte aligned).
-int bwd_impl(const FpaBwdArgs *a, void *wsp, void *stream) {
+// with their scratch regions carved out of `wsp` (fpa_bwd_workspace_bytes bytes, 256-byte aligned;
+// with split_ok false, the layout without split tiles).
+int bwd_impl(const FpaBwdArgs *a, void *wsp, void *stream, bool split_ok = true) {
     int rc = check_common(a->B, a->H, a->T, a->D, a->dtype, a->tau);
     if (rc) return rc;
     if ((rc = check_rows(a->q, a->sq, a->dtype, "q")) || (rc = check_rows(a->k, a->sk, a->dtype, "k")) ||
@@ -282,7 +284,7 @@ int bwd_impl(const FpaBwdArgs *a, void *wsp, void *stream) {
         return fail(FPA_ERR_INVALID, "beta, lse, state, dphi, dpsi and dbeta must be non-NULL");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int64_t TP = tp_of(a->T);
-    const WsLayout wl = ws_layout(a->B, a->H, a->T, a->D, a->dtype);
+    const WsLayout wl = ws_layout(a->B, a->H, a->T, a->D, a->dtype, split_ok);
     float *ws = static_cast<float *>(wsp);
     BwdParams p;
     p.q = a->q; p.sq = s3(a->sq);
@@ -379,7 +381,10 @@ int fpa_bwd_noalloc(const FpaBwdArgs *a, void *stream) {
     if (a == nullptr) return fail(FPA_ERR_INVALID, "args is NULL");
     int rc = check_common(a->B, a->H, a->T, a->D, a->dtype, a->tau);
     if (rc) return rc;
-    const int64_t need = ws_layout(a->B, a->H, a->T, a->D, a->dtype).total * (int64_t)sizeof(float);
+    // The partial sums of split tiles are left out (every tile whole) when they alone would not fit.
+    const bool split_ok = ws_layout(a->B, a->H, a->T, a->D, a->dtype).total * (int64_t)sizeof(float) <=
+                          FPA_NOALLOC_SCRATCH_BYTES;
+    const int64_t need = ws_layout(a->B, a->H, a->T, a->D, a->dtype, split_ok).total * (int64_t)sizeof(float);
     if (need > FPA_NOALLOC_SCRATCH_BYTES)
         return fail(FPA_ERR_UNSUPPORTED, "fpa_bwd_noalloc: this problem needs " + std::to_string(need) +
                                              " bytes of scratch, more than the " +
@@ -387,7 +392,7 @@ int fpa_bwd_noalloc(const FpaBwdArgs *a, void *stream) {
                                              " it holds; call fpa_bwd with a workspace");
     void *ws = scratch_of_current_device();
     if (ws == nullptr) return FPA_ERR_HIP;
-    return bwd_impl(a, ws, stream);
+    return bwd_impl(a, ws, stream, split_ok);
 }
 
 }  // extern "C"

@@ -178,9 +178,10 @@ int fpa_bwd(const FpaBwdArgs *args, void *stream);
 
 /* The backward without a caller workspace, for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart
- * in the reference.  Same arguments and results as fpa_bwd (args->workspace is ignored); the
- * scratch is a static device array of FPA_NOALLOC_SCRATCH_BYTES per GPU, held until the process
- * ends.  Problems whose fpa_bwd_workspace_bytes exceed it return FPA_ERR_UNSUPPORTED before any
+ * in the reference.  Same arguments and results as fpa_bwd (args->workspace is ignored; should the
+ * partial sums of a small launch's split tiles not fit, every tile runs whole, the same results to
+ * rounding); the scratch is a static device array of FPA_NOALLOC_SCRATCH_BYTES per GPU, held until
+ * the process ends.  Problems whose fpa_bwd_workspace_bytes exceed it return FPA_ERR_UNSUPPORTED before any
  * launch.  Calls that overlap on one GPU (two streams, two threads) share that array and race:
  * serialise them.  Allocates nothing (no hipMalloc or allocating library routine).            */
 #define FPA_NOALLOC_SCRATCH_BYTES (64ll << 20)
