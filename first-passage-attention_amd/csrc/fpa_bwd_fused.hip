@@ -75,8 +75,8 @@ fpa_bwd_kvq_split_kernel(BwdParams p, BwdOrder ord, int nslots) {
         bwd_kv_tile<T, D, NW, true>(p, sm.kv, tile, bh, 0, half);
 }
 
-// Whether the fused launch applies at this shape (both sides one launch shape, one dK / dV part, not
-// fp32 at D = 64, at most FUSED_MAX slots per head).
+// Whether the fused launch applies to this dtype and D (both sides one launch shape, one dK / dV part,
+// not fp32 at D = 64); it also needs at most FUSED_MAX slots per head.
 template <typename T, int D>
 constexpr bool kvq_fused() {
     return kv_wpe<T, D>() == q_wpe<T, D>() && kv_parts<T, D>() == 1 && !(sizeof(T) == 4 && D == 64);
