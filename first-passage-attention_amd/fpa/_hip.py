@@ -9,6 +9,7 @@ multiple of the block and no ``.contiguous()`` copy for the layer's permuted vie
 a tensor is copied only when its head dimension is not contiguous or its rows are
 not 16-byte aligned.
 """
+import contextlib
 import functools
 
 import torch
@@ -38,6 +39,13 @@ def _rows_ok(t):
     s = t.stride()
     return (s[3] == 1 and t.data_ptr() % 16 == 0 and all(x % ce == 0 for x in s[:3])
             and 0 <= s[2] * 64 * t.element_size() < 2 ** 31)
+
+
+def device_guard(dev):
+    """torch.cuda.device(dev), or nothing to enter when dev is already the current device."""
+    if dev.index is None or dev.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(dev)
 
 
 def rows(t):
@@ -90,59 +98,39 @@ class BwdBuffers:
     def __init__(self, q, dqkv=None):
         B, H, T, D = q.shape
         dev = q.device
-        if dqkv is None:
-            self.dq = torch.empty((B, H, T, D), dtype=q.dtype, device=dev)
-            self.dk = torch.empty_like(self.dq)
-            self.dv = torch.empty_like(self.dq)
+        if dqkv is None:  # one allocation for the three
+            self.dq, self.dk, self.dv = torch.empty((3, B, H, T, D), dtype=q.dtype, device=dev).unbind(0)
         else:  # strided views of one (B, T, 3, H, D) buffer
             self.dq, self.dk, self.dv = dqkv.permute(2, 0, 3, 1, 4)
-        self.dphi = torch.empty((B, H, T), dtype=torch.float32, device=dev)
-        self.dpsi = torch.empty_like(self.dphi)
-        self.dbeta = torch.empty(H, dtype=torch.float32, device=dev)
+        n = B * H * T
+        f = torch.empty(2 * n + H, dtype=torch.float32, device=dev)  # dphi, dpsi, dbeta in one allocation
+        self.dphi, self.dpsi = f[:n].view(B, H, T), f[n:2 * n].view(B, H, T)
+        self.dbeta = f[2 * n:]
         self.ws = workspace(dev, _bwd_ws_bytes(B, H, T, D, _lib.dtype_code(q.dtype)))
 
 
 def fwd_args(q, k, v, phi, psi, beta, tau, out):
     """FpaFwdArgs for fpa_fwd (q/k/v already passed through rows(); phi, psi, beta float32)."""
     B, H, T, D = q.shape
-    a = _lib.FpaFwdArgs()
-    a.B, a.H, a.T, a.D = B, H, T, D
-    a.dtype = _lib.dtype_code(q.dtype)
-    a.tau = float(tau)
-    a.q, a.sq = _lib.ptr(q), _lib.strides4(q)
-    a.k, a.sk = _lib.ptr(k), _lib.strides4(k)
-    a.v, a.sv = _lib.ptr(v), _lib.strides4(v)
-    a.phi, a.sphi = _lib.ptr(phi), _lib.strides3(phi)
-    a.psi, a.spsi = _lib.ptr(psi), _lib.strides3(psi)
-    a.beta = _lib.ptr(beta)
-    a.o, a.so = _lib.ptr(out.o), _lib.strides4(out.o)
-    a.lse, a.state = _lib.ptr(out.lse), _lib.ptr(out.state)
-    a.phases = 0
-    a.workspace = _lib.ptr(out.ws) if out.ws is not None else None
-    return a
+    o, ws = out.o, out.ws
+    return _lib.FpaFwdArgs.from_buffer_copy(_lib.FWD_PACK.pack(
+        B, H, T, D, _lib.dtype_code(q.dtype), float(tau),
+        q.data_ptr(), *q.stride(), k.data_ptr(), *k.stride(), v.data_ptr(), *v.stride(),
+        phi.data_ptr(), *phi.stride(), psi.data_ptr(), *psi.stride(), beta.data_ptr(),
+        o.data_ptr(), *o.stride(), out.lse.data_ptr(), out.state.data_ptr(), 0,
+        ws.data_ptr() if ws is not None else 0))
 
 
 def bwd_args(q, k, v, beta, tau, fwd, do, grads):
     """FpaBwdArgs for fpa_bwd."""
     B, H, T, D = q.shape
-    a = _lib.FpaBwdArgs()
-    a.B, a.H, a.T, a.D = B, H, T, D
-    a.dtype = _lib.dtype_code(q.dtype)
-    a.tau = float(tau)
-    a.q, a.sq = _lib.ptr(q), _lib.strides4(q)
-    a.k, a.sk = _lib.ptr(k), _lib.strides4(k)
-    a.v, a.sv = _lib.ptr(v), _lib.strides4(v)
-    a.beta = _lib.ptr(beta)
-    a.o, a.so = _lib.ptr(fwd.o), _lib.strides4(fwd.o)
-    a.dout, a.sdo = _lib.ptr(do), _lib.strides4(do)
-    a.lse, a.state = _lib.ptr(fwd.lse), _lib.ptr(fwd.state)
-    a.dq, a.sdq = _lib.ptr(grads.dq), _lib.strides4(grads.dq)
-    a.dk, a.sdk = _lib.ptr(grads.dk), _lib.strides4(grads.dk)
-    a.dv, a.sdv = _lib.ptr(grads.dv), _lib.strides4(grads.dv)
-    a.dphi, a.dpsi, a.dbeta = _lib.ptr(grads.dphi), _lib.ptr(grads.dpsi), _lib.ptr(grads.dbeta)
-    a.workspace = _lib.ptr(grads.ws)
-    a.phases = 0
-    return a
+    o, dq, dk, dv = fwd.o, grads.dq, grads.dk, grads.dv
+    return _lib.FpaBwdArgs.from_buffer_copy(_lib.BWD_PACK.pack(
+        B, H, T, D, _lib.dtype_code(q.dtype), float(tau),
+        q.data_ptr(), *q.stride(), k.data_ptr(), *k.stride(), v.data_ptr(), *v.stride(), beta.data_ptr(),
+        o.data_ptr(), *o.stride(), do.data_ptr(), *do.stride(), fwd.lse.data_ptr(), fwd.state.data_ptr(),
+        dq.data_ptr(), *dq.stride(), dk.data_ptr(), *dk.stride(), dv.data_ptr(), *dv.stride(),
+        grads.dphi.data_ptr(), grads.dpsi.data_ptr(), grads.dbeta.data_ptr(), grads.ws.data_ptr(), 0))
 
 
 def run_fwd(args, device):
@@ -171,7 +159,7 @@ class FirstPassageAttentionHIP(torch.autograd.Function):
         q, k, v = rows(q), rows(k), rows(v)
         beta = beta.contiguous()
         dev = q.device
-        with torch.cuda.device(dev):
+        with device_guard(dev):
             out = FwdBuffers(q)
             run_fwd(fwd_args(q, k, v, phi, psi, beta, tau, out), dev)
         ctx.save_for_backward(q, k, v, out.o, out.lse, out.state, beta)
@@ -183,7 +171,7 @@ class FirstPassageAttentionHIP(torch.autograd.Function):
         q, k, v, o, lse, state, beta = ctx.saved_tensors
         dev = q.device
         do = rows(do.to(q.dtype))
-        with torch.cuda.device(dev):
+        with device_guard(dev):
             grads = BwdBuffers(q)
             run_bwd(bwd_args(q, k, v, beta, ctx.tau, _Saved(o, lse, state), do, grads), dev)
         return grads.dq, grads.dk, grads.dv, grads.dphi, grads.dpsi, grads.dbeta, None
@@ -200,7 +188,7 @@ class FirstPassageAttentionPackedHIP(torch.autograd.Function):
         q, k, v = (rows(t) for t in qkv.permute(2, 0, 3, 1, 4))
         beta = beta.contiguous()
         dev = qkv.device
-        with torch.cuda.device(dev):
+        with device_guard(dev):
             o_bthd = torch.empty((B, T, H, D), dtype=qkv.dtype, device=dev)
             out = FwdBuffers(q, o=o_bthd.permute(0, 2, 1, 3))
             run_fwd(fwd_args(q, k, v, phi, psi, beta, tau, out), dev)
@@ -214,7 +202,7 @@ class FirstPassageAttentionPackedHIP(torch.autograd.Function):
         B, H, T, D = q.shape
         dev = q.device
         do = rows(do_bthd.to(q.dtype).permute(0, 2, 1, 3))
-        with torch.cuda.device(dev):
+        with device_guard(dev):
             dqkv = torch.empty((B, T, 3, H, D), dtype=q.dtype, device=dev)
             grads = BwdBuffers(q, dqkv=dqkv)
             run_bwd(bwd_args(q, k, v, beta, ctx.tau, _Saved(o, lse, state), do, grads), dev)
@@ -238,7 +226,7 @@ class FieldHIP(torch.autograd.Function):
         b = bias.float().contiguous()
         L = _lib.lib()
         dev = x.device
-        with torch.cuda.device(dev):
+        with device_guard(dev):
             phi = torch.empty((B, n_heads, T), dtype=torch.float32, device=dev)
             psi = torch.empty_like(phi)
             ws = torch.empty(L.fpa_field_workspace_bytes(B, T, C, n_heads), dtype=torch.uint8, device=dev)
@@ -266,7 +254,7 @@ class FieldHIP(torch.autograd.Function):
         dphi = zeros if dphi is None else dphi.float().contiguous()
         dpsi = zeros if dpsi is None else dpsi.float().contiguous()
         L = _lib.lib()
-        with torch.cuda.device(dev):
+        with device_guard(dev):
             dx = torch.empty_like(x) if ctx.needs_input_grad[0] else None
             dw = torch.empty_like(w)
             db = torch.empty(w.shape[0], dtype=torch.float32, device=dev)

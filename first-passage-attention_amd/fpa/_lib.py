@@ -6,6 +6,7 @@ library raises, so ``impl="hip"`` can never run on anything but the HIP kernels.
 """
 import ctypes
 import os
+import struct
 import warnings
 
 import torch
@@ -46,6 +47,13 @@ class FpaBwdArgs(ctypes.Structure):
                 ("dphi", _vp), ("dpsi", _vp), ("dbeta", _vp), ("workspace", _vp),
                 ("phases", ctypes.c_int32)]
 
+
+# Byte images of the two argument structs, field after field as include/fpa.h lays them out (64-bit
+# host: 8-byte pointers and int64, 4-byte int32 and float, the struct padded to 8 bytes): one pack call
+# fills a struct instead of one ctypes assignment per field.
+FWD_PACK = struct.Struct("=qqqqif" + "q4q" * 3 + "q3q" * 2 + "q" + "q4q" + "qq" + "i4x" + "q")
+BWD_PACK = struct.Struct("=qqqqif" + "q4q" * 3 + "q" + "q4q" * 2 + "qq" + "q4q" * 3 + "qqqq" + "i4x")
+assert FWD_PACK.size == ctypes.sizeof(FpaFwdArgs) and BWD_PACK.size == ctypes.sizeof(FpaBwdArgs)
 
 _S2 = _i64 * 2
 
@@ -147,11 +155,3 @@ def stream_of(device):
 def ptr(t):
     """Device address of t for a pointer field of an argument struct (an int: ctypes converts it)."""
     return t.data_ptr()
-
-
-def strides4(t):
-    return _S4(*t.stride())
-
-
-def strides3(t):
-    return _S3(*t.stride())

@@ -60,6 +60,49 @@ def test_struct_layout_matches_header(tmp_path):
         assert got == int(val), (cname, field, got, val)
 
 
+def test_packed_args_equal_the_ctypes_structs():
+    """fwd_args / bwd_args fill the argument structs with one struct.pack; the bytes are those of the
+    same structs filled field by field through the ctypes mirrors (whose layout is checked against
+    the header above), for strided tensors and with and without a forward workspace."""
+    from fpa import _hip
+    g = torch.Generator().manual_seed(0)
+    base = torch.randn(2, 5, 3, 3, 16, generator=g).half()  # (B, T, 3, H, D)
+    q, k, v = base.permute(2, 0, 3, 1, 4)  # (B, H, T, D) = (2, 3, 5, 16) views with the layer's strides
+    do, o = torch.randn(2, 3, 5, 16).half(), torch.randn(2, 3, 5, 16).half()
+    phi, psi = torch.randn(2, 3, 9)[..., :5], torch.randn(2, 3, 5)
+    beta = torch.randn(3)
+
+    class Buf:
+        pass
+    fb = Buf()
+    fb.o, fb.lse, fb.state = o, torch.empty(64), torch.empty(32)
+    gb = Buf()
+    gb.dq, gb.dk, gb.dv = torch.empty((3, 2, 3, 5, 16), dtype=torch.float16).unbind(0)
+    gb.dphi, gb.dpsi, gb.dbeta, gb.ws = torch.empty(2, 3, 5), torch.empty(2, 3, 5), torch.empty(3), torch.empty(8)
+    S4 = ctypes.c_int64 * 4
+    S3 = ctypes.c_int64 * 3
+    for ws in (None, torch.empty(16)):
+        fb.ws = ws
+        a = _lib.FpaFwdArgs()
+        a.B, a.H, a.T, a.D, a.dtype, a.tau = 2, 3, 5, 16, 0, 0.75
+        a.q, a.sq, a.k, a.sk, a.v, a.sv = q.data_ptr(), S4(*q.stride()), k.data_ptr(), S4(*k.stride()), v.data_ptr(), S4(*v.stride())
+        a.phi, a.sphi, a.psi, a.spsi = phi.data_ptr(), S3(*phi.stride()), psi.data_ptr(), S3(*psi.stride())
+        a.beta, a.o, a.so = beta.data_ptr(), o.data_ptr(), S4(*o.stride())
+        a.lse, a.state, a.phases = fb.lse.data_ptr(), fb.state.data_ptr(), 0
+        a.workspace = ws.data_ptr() if ws is not None else None
+        assert bytes(_hip.fwd_args(q, k, v, phi, psi, beta, 0.75, fb)) == bytes(a)
+    b = _lib.FpaBwdArgs()
+    b.B, b.H, b.T, b.D, b.dtype, b.tau = 2, 3, 5, 16, 0, 0.75
+    b.q, b.sq, b.k, b.sk, b.v, b.sv = q.data_ptr(), S4(*q.stride()), k.data_ptr(), S4(*k.stride()), v.data_ptr(), S4(*v.stride())
+    b.beta, b.o, b.so, b.dout, b.sdo = beta.data_ptr(), o.data_ptr(), S4(*o.stride()), do.data_ptr(), S4(*do.stride())
+    b.lse, b.state = fb.lse.data_ptr(), fb.state.data_ptr()
+    b.dq, b.sdq, b.dk, b.sdk = gb.dq.data_ptr(), S4(*gb.dq.stride()), gb.dk.data_ptr(), S4(*gb.dk.stride())
+    b.dv, b.sdv = gb.dv.data_ptr(), S4(*gb.dv.stride())
+    b.dphi, b.dpsi, b.dbeta, b.workspace, b.phases = (gb.dphi.data_ptr(), gb.dpsi.data_ptr(), gb.dbeta.data_ptr(),
+                                                      gb.ws.data_ptr(), 0)
+    assert bytes(_hip.bwd_args(q, k, v, beta, 0.75, fb, do, gb)) == bytes(b)
+
+
 def test_size_queries():
     L = _lib.lib()
     B, H, T = 2, 3, 100
