@@ -149,6 +149,33 @@ def fpa_grads_stored(q, k, v, phi, psi, beta, do, tau=1.0, store=torch.float16, 
     return [o.detach()] + [g.detach() for g in grads]
 
 
+def dbeta_terms(q, k, v, phi, psi, beta, do, tau=1.0, dtype=torch.float64):
+    """Per head, dbeta = sum_{s<=t} dS_ts min(0, x_ts) and the magnitude A of what it is made of.
+
+    x_ts = min phi(s, t] - psi_s: the bias's value is beta * min(0, x) (kernel.py:44-54), so
+    d bias / d beta = min(0, x); the reference's _bwd_kv adds dS x over its key blocks at
+    kernel.py:227, 249.  dS_ts = P_ts dP_ts - P_ts Delta_t with dP = dO V^T and Delta_t = sum_d dO_td
+    O_td.  A = sum |P_ts min(0, x_ts)| (|dP_ts| + |Delta_t|) bounds how far relative errors of at most e
+    in every dP_ts and Delta_t (the arithmetic's own rounding, or the rounding of the stored output
+    that Delta is taken from) can move dbeta: by at most e * A.  Where the two products cancel (A much
+    larger than |dbeta|), rounding at the level of the arithmetic alone moves dbeta by that much.
+    Returns (dbeta, A), each of shape (H,).
+    """
+    H, T, D = q.shape[1], q.shape[2], q.shape[3]
+    b = beta if torch.is_tensor(beta) else torch.tensor(float(beta))
+    b = b.reshape(-1)
+    if b.numel() == 1:
+        b = b.expand(H)
+    qd, kd, vd, ph, ps, dod = [t.detach().cpu().to(dtype) for t in (q, k, v, phi, psi, do)]
+    xm = (range_min(ph) - ps.unsqueeze(-2)).clamp(max=0.0)  # [t, s]; empty range: +inf -> 0
+    causal = torch.ones(T, T, dtype=torch.bool).tril()
+    logits = torch.matmul(qd, kd.transpose(-1, -2)) / math.sqrt(D) + b.detach().cpu().to(dtype).reshape(-1, 1, 1) * xm
+    p = torch.softmax(logits.masked_fill(~causal, -math.inf), dim=-1)
+    dp = torch.matmul(dod, vd.transpose(-1, -2))
+    delta = (dod * torch.matmul(p, vd)).sum(-1, keepdim=True)
+    px = (p * xm).masked_fill(~causal, 0.0)
+    return (px * (dp - delta)).sum((0, 2, 3)), (px.abs() * (dp.abs() + delta.abs())).sum((0, 2, 3))
+
 def fpa_grads_chunked(q, k, v, phi, psi, beta, do, tau=1.0, dtype=torch.float64, device=None,
                       max_elems=1 << 27):
     """fpa_grads computed over chunks of query rows, for shapes whose (T, T) tensors are too big.

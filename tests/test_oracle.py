@@ -215,3 +215,29 @@ def test_stored_output_oracle():
         assert np.allclose(other[1][0, h].numpy() - exact[1][0, h].numpy(), change @ kd[0, h] / np.sqrt(D),
                            rtol=1e-6, atol=1e-12)
         assert np.allclose(other[3][0, h].numpy(), exact[3][0, h].numpy(), rtol=1e-11, atol=1e-12)
+
+
+@pytest.mark.parametrize("seed,scale,sign", [(5, 1.0, 1.0), (6, 4.0, -1.0), (7, 0.3, 1.0)])
+def test_dbeta_terms(seed, scale, sign):
+    """dbeta_terms: its dbeta is autograd's (through the straight-through bias), and its magnitude is the
+    loop definition's sum_{s<t} |min(0, x_ts) P_ts| (|dP_ts| + |Delta_t|) with P, dP and Delta from the
+    closed-form softmax backward (the pairs s = t add 0: the bias is 0 there); it bounds |dbeta|."""
+    B, H, T, D = 1, 2, 23, 16
+    q, k, v, phi, psi, beta, do = O.make_inputs(B, H, T, D, dtype=torch.float32, seed=seed, phi_scale=scale)
+    beta = sign * beta
+    tot, mag = O.dbeta_terms(q, k, v, phi, psi, beta, do, tau=0.8)
+    ref = O.fpa_grads(q, k, v, phi, psi, beta, do, tau=0.8)[6]
+    assert O.rel_err(tot, ref) <= 1e-12
+    assert (mag >= tot.abs() - 1e-12).all()
+    qd, kd, vd, dod, ph, ps = (t.double().numpy() for t in (q, k, v, do, phi, psi))
+    bias = O.bias_by_loops(ph, ps, beta.double().numpy())
+    for h in range(H):
+        z = qd[0, h] @ kd[0, h].T / np.sqrt(D) + bias[0, h]
+        z = np.where(np.tril(np.ones((T, T), bool)), z, -np.inf)
+        p = np.exp(z - z.max(-1, keepdims=True))
+        p /= p.sum(-1, keepdims=True)
+        dp = dod[0, h] @ vd[0, h].T
+        delta = (dod[0, h] * (p @ vd[0, h])).sum(-1)
+        loop = sum(abs(min(0.0, ph[0, h, s + 1:t + 1].min() - ps[0, h, s]) * p[t, s]) * (abs(dp[t, s]) + abs(delta[t]))
+                   for t in range(T) for s in range(t))
+        assert abs(mag[h].item() - loop) <= 1e-12 * loop
