@@ -429,7 +429,10 @@ def main():
     ref_fwd, ref_fwd_rounds = time_ref_protocol(fwd, a.rounds)
     ref_fb, ref_fb_rounds = time_ref_protocol(step_with_clones, a.rounds)
 
-    # Per-kernel durations: one C-ABI call per kernel (phases), HIP events on the launch stream.
+    # Per-kernel durations: one C-ABI call per kernel (phases), HIP events on the launch stream, each
+    # kernel (a) in the order of a step, one event after each call, so that it starts from the caches
+    # the kernel before it left, as inside the timed steps and a kernel trace of them, and (b) repeated
+    # alone, its inputs warm in the caches.
     qr, kr, vr = _hip.rows(q), _hip.rows(k), _hip.rows(v)
     phi32, psi32, beta32 = phi.float().contiguous(), psi.float().contiguous(), beta.float().contiguous()
     fb = _hip.FwdBuffers(qr)
@@ -454,15 +457,34 @@ def main():
 
     P = pairs(cfg)
     D = cfg["D"]
-    # The kernels of a step, with their algorithmic flops.
-    kernels = {
-        "fpa_stats": (time_call(fa, _hip.run_fwd, _lib.FPA_FWD_STATS), 0),
-        "fpa_fwd_kernel": (time_call(fa, _hip.run_fwd, _lib.FPA_FWD_MAIN), 4 * D * P),
-    }
-    for name, phases, flops in BWD_KERNELS:
-        kernels[name] = (time_call(ba, _hip.run_bwd, phases), flops * D * P)
-    if fb.ws is not None:  # split row tiles: their merge (reads and rewrites o, so timed after the rest)
-        kernels["fpa_fwd_merge"] = (time_call(fa, _hip.run_fwd, _lib.FPA_FWD_MERGE), 0)
+    # The kernels of a step in their order, with their algorithmic flops.
+    seq = [("fpa_stats", fa, _hip.run_fwd, _lib.FPA_FWD_STATS, 0),
+           ("fpa_fwd_kernel", fa, _hip.run_fwd, _lib.FPA_FWD_MAIN, 4 * D * P)]
+    if fb.ws is not None:  # split row tiles: their merge
+        seq.append(("fpa_fwd_merge", fa, _hip.run_fwd, _lib.FPA_FWD_MERGE, 0))
+    seq += [(name, ba, _hip.run_bwd, phases, flops * D * P) for name, phases, flops in BWD_KERNELS]
+
+    def time_sequence(reps):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(seq) + 1)]
+        tot = [0.0] * len(seq)
+        for r in range(reps + 1):  # the first pass untimed
+            ev[0].record()
+            for i, (_, args, runner, phases, _) in enumerate(seq):
+                args.phases = phases
+                runner(args, dev)
+                ev[i + 1].record()
+            ev[-1].synchronize()
+            if r:
+                for i in range(len(seq)):
+                    tot[i] += ev[i].elapsed_time(ev[i + 1])
+        fa.phases = ba.phases = 0
+        return [x / reps for x in tot]
+
+    in_seq = time_sequence(a.kernel_reps)
+    kernels = {name: (ms, flops) for (name, _, _, _, flops), ms in zip(seq, in_seq)}
+    # Alone: the merge reads and rewrites o, so it goes after the rest.
+    order = [s for s in seq if s[0] != "fpa_fwd_merge"] + [s for s in seq if s[0] == "fpa_fwd_merge"]
+    alone = {name: time_call(args, runner, phases) for name, args, runner, phases, _ in order}
     dom = max(kernels, key=lambda n: kernels[n][0])
     dom_ms, dom_flops = kernels[dom]
     peak = PEAK_TFLOPS[cfg["dtype"]]
@@ -525,6 +547,7 @@ def main():
                                      "calls, synchronised after each); fwd+bwd clones the inputs "
                                      "(reference bench.py:11-23, 44-54)"},
         "kernel_ms": {n: round(t, 4) for n, (t, _) in kernels.items()},
+        "kernel_ms_alone": {n: round(t, 4) for n, t in alone.items()},
         "roofline": roofline(a.config, custom, dom, dom_ms, dom_flops, peak),
         "configs": extra,
         "cpu_baseline": cpu,
