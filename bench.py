@@ -464,21 +464,22 @@ def main():
         seq.append(("fpa_fwd_merge", fa, _hip.run_fwd, _lib.FPA_FWD_MERGE, 0))
     seq += [(name, ba, _hip.run_bwd, phases, flops * D * P) for name, phases, flops in BWD_KERNELS]
 
-    def time_sequence(reps):
+    def time_sequence(reps, warm=3):
+        """Median over `reps` sequences (after `warm` untimed ones) of each kernel's event-to-event time."""
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(seq) + 1)]
-        tot = [0.0] * len(seq)
-        for r in range(reps + 1):  # the first pass untimed
+        samples = [[] for _ in seq]
+        for r in range(warm + reps):
             ev[0].record()
             for i, (_, args, runner, phases, _) in enumerate(seq):
                 args.phases = phases
                 runner(args, dev)
                 ev[i + 1].record()
             ev[-1].synchronize()
-            if r:
+            if r >= warm:
                 for i in range(len(seq)):
-                    tot[i] += ev[i].elapsed_time(ev[i + 1])
+                    samples[i].append(ev[i].elapsed_time(ev[i + 1]))
         fa.phases = ba.phases = 0
-        return [x / reps for x in tot]
+        return [statistics.median(s) for s in samples]
 
     in_seq = time_sequence(a.kernel_reps)
     kernels = {name: (ms, flops) for (name, _, _, _, flops), ms in zip(seq, in_seq)}
