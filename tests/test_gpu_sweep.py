@@ -58,7 +58,7 @@ pytestmark = pytest.mark.gpu
 
 def _cases(n=16, seed=2026, lengths=(1, 37, 64, 129, 200, 333, 512, 701), first=1000,
            betas=("positive", "negative", "mixed", "zero"), dims=(16, 32, 64, 128), ties=False,
-           dtypes=("f16", "f32"), taus=(0.5, 1.0, 2.0)):
+           dtypes=("f16", "f32"), taus=(0.5, 1.0, 2.0), scales=(0.3, 1.0, 4.0)):
     rng = random.Random(seed)
     out = []
     for i in range(n):
@@ -69,7 +69,7 @@ def _cases(n=16, seed=2026, lengths=(1, 37, 64, 129, 200, 333, 512, 701), first=
             dtype=rng.choice(dtypes),
             beta=rng.choice(betas),
             tau=rng.choice(taus),
-            phi_scale=rng.choice([0.3, 1.0, 4.0]),
+            phi_scale=rng.choice(scales),
             drift=rng.choice([0.0, 0.02]),
             psi_noise=rng.choice([0.1, 0.25, 0.5]),
             ties=ties,
@@ -83,7 +83,9 @@ def _cases(n=16, seed=2026, lengths=(1, 37, 64, 129, 200, 333, 512, 701), first=
 # long fp16 draws with beta of either sign; six at extreme temperatures (tau 0.1: the soft-min weights
 # near one-hot over spans of a few units of phi; tau 8: near-uniform); four long fp32 draws with
 # negative or mixed beta; then a wider draw of 100 over lengths up to 2500 and every head dimension, and
-# 25 long draws at tau 0.1 to 8 (six of these have dbeta sums that cancel by 5e3 to 5e5).
+# 25 long draws at tau 0.1 to 8 (six of these have dbeta sums that cancel by 5e3 to 5e5); then 24 at phi
+# scales 10 to 40 (soft-min spreads past the product form's range and the in-block recurrence's single
+# reference).
 CASES = (_cases() + _cases(n=6, seed=7, lengths=(1000, 1531, 2048), first=2000, betas=("positive",))
          + _cases(n=6, seed=11, lengths=(3, 65, 190, 449, 640), first=3000, dims=(256,))
          + _cases(n=6, seed=13, lengths=(97, 256, 511, 800), first=4000, ties=True)
@@ -93,7 +95,9 @@ CASES = (_cases() + _cases(n=6, seed=7, lengths=(1000, 1531, 2048), first=2000, 
                   dims=(16, 32, 64))
          + _cases(n=100, seed=31337, lengths=(1, 17, 63, 65, 127, 129, 255, 383, 385, 511, 640, 897, 1025, 1500, 2047,
                                              2500), first=90000, dims=(16, 32, 64, 128, 256))
-         + _cases(n=25, seed=31339, lengths=(450, 999, 1800), first=92000, taus=(0.1, 0.25, 4.0, 8.0)))
+         + _cases(n=25, seed=31339, lengths=(450, 999, 1800), first=92000, taus=(0.1, 0.25, 4.0, 8.0))
+         + _cases(n=24, seed=41, lengths=(33, 100, 257, 600, 1100), first=93000, dims=(16, 32, 64, 128, 256),
+                  taus=(0.3, 1.0, 3.0), scales=(10.0, 20.0, 40.0)))
 
 
 def _say(*a):
