@@ -22,8 +22,9 @@
 #ifndef FPA_FWD_WPE32
 #define FPA_FWD_WPE32 2
 #endif
-// fp16: the scores of each 32-key half computed just before its softmax (13 fewer live registers at
-// D = 64, 1-4% faster at cfg2) instead of both halves' MFMA chains interleaved up front.
+// The scores of each 32-key half computed just before its softmax instead of both halves' MFMA chains
+// interleaved up front: fp16 at D <= 64 (13 fewer live registers at D = 64, 1-4% faster at cfg2) and
+// fp32 at D = 256 (see the kernel).
 #ifndef FPA_FWD_SPLIT
 #define FPA_FWD_SPLIT 1
 #endif
@@ -168,7 +169,9 @@ fpa_fwd_kernel(FwdParams p) {
             // Both 32-key halves' scores first; then each half in turn (the second half's MFMAs
             // and the first half's P V run while the other half's VALU work goes on).
             f32x16 s[2];
-            constexpr bool SPLIT = FPA_FWD_SPLIT && sizeof(T) == 2 && D <= 64;  // measured there (3 waves per SIMD)
+            // Measured: fp16 at D <= 64 (3 waves per SIMD) and fp32 at D = 256 (20 fewer spilled registers,
+            // 3% faster); level or slower for the other shapes.
+            constexpr bool SPLIT = FPA_FWD_SPLIT && ((sizeof(T) == 2 && D <= 64) || (sizeof(T) == 4 && D == 256));
             if constexpr (!SPLIT) {
                 s[0] = zero16();
                 s[1] = zero16();
