@@ -122,8 +122,9 @@ inline bool supported_d(int dtype, int D) {
     return D == 16 || D == 32 || D == 64 || D == 128 || D == 256;
 }
 
-// Most 64-blocks of T: T <= 2097152.  The backward workspace holds 4 bytes per block pair (TBUF), 4 GiB
-// per head at this cap.
-constexpr int MAX_NB = 32768;
+// Most 64-blocks of T: T <= 4194304.  The backward workspace holds 4 bytes per block pair (TBUF), 16 GiB
+// per head at this cap; every index into it is 64-bit, and the 32-bit counts derived from the block
+// count (the combine's pair count, at most (NB / 2)^2 = 2^30) stay below 2^31.
+constexpr int MAX_NB = 65536;
 
 }  // namespace fpa
