@@ -249,9 +249,12 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
     for (int k = 0; k < 16; ++k) gq[k] = contrib[lane][16 * w + k];
     const float cU = -ld_uniform(p.state, L.bplane(BP_MIN) + brow + U) * il2;  // sBM[U]
     const int nI = NB - 1 - U;
-    const int npairs = U * nI;
+    // (query block after U, key block before U) pairs: some exist when U > 0 and nI > 0; their count is
+    // needed only by the pair loop below MID_SCAN_NB blocks, where it is small (at most (NB / 2)^2).
+    const bool haspairs = U > 0 && nI > 0;
+    const int npairs = midscan ? 0 : U * nI;
     float SU = 0.f;
-    if (npairs > 0) {  // uniform: U is the workgroup's block
+    if (haspairs) {  // uniform: U is the workgroup's block
         // scanA[i] = max over [i, U), scanB[i] = max over (U, i]; waves 0 and 1 in parallel.
         if (!midscan) {
             if (w == 0) wave_suffix_max(scanA, sBM, NB, U, lane);
@@ -461,7 +464,7 @@ __global__ void __launch_bounds__(NTHREADS) fpa_bwd_combine_kernel(BwdParams p) 
         const int u = lane;
         if (u <= last) {
             float tot = ((pp[0][u] + pp[1][u]) + (pp[2][u] + pp[3][u]));
-            if (npairs > 0) tot += fexp2(sA[u] - cU) * SU;
+            if (haspairs) tot += fexp2(sA[u] - cU) * SU;
             p.dphi[(int64_t)bh * p.T + sb + u] = p.beta[h] * tot;
         }
     }

@@ -122,9 +122,9 @@ inline bool supported_d(int dtype, int D) {
     return D == 16 || D == 32 || D == 64 || D == 128 || D == 256;
 }
 
-// Most 64-blocks of T: T <= 4194304.  The backward workspace holds 4 bytes per block pair (TBUF), 16 GiB
-// per head at this cap; every index into it is 64-bit, and the 32-bit counts derived from the block
-// count (the combine's pair count, at most (NB / 2)^2 = 2^30) stay below 2^31.
-constexpr int MAX_NB = 65536;
+// Most 64-blocks of T: T <= 8388608.  The backward workspace holds 4 bytes per block pair (TBUF), 64 GiB
+// per head at this cap; every index into it is 64-bit, and the 32-bit values derived from the block count
+// stay below 2^31 (positions, workgroup ids, 32-bit offsets of at most ten planes of TP floats).
+constexpr int MAX_NB = 131072;
 
 }  // namespace fpa

@@ -54,7 +54,7 @@ extern "C" {
 /* status codes */
 #define FPA_OK 0
 #define FPA_ERR_INVALID 1     /* invalid argument (shape, dtype, tau, stride)        */
-#define FPA_ERR_UNSUPPORTED 2 /* valid for the reference but not built (e.g. D > 256, T > 4194304) */
+#define FPA_ERR_UNSUPPORTED 2 /* valid for the reference but not built (e.g. D > 256, T > 8388608) */
 #define FPA_ERR_HIP 3         /* a HIP runtime call failed                            */
 
 /* Forward arguments.  Tensors are (B, H, T, D) for q/k/v/o and (B, H, T) for

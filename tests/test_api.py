@@ -119,7 +119,7 @@ def test_size_queries():
     ("dtype", 7, _lib.FPA_ERR_INVALID, "q, k and v must all be fp16 or all fp32"),
     ("D", 512, _lib.FPA_ERR_UNSUPPORTED, "head dimension 512 is not built"),
     ("T", 0, _lib.FPA_ERR_INVALID, "q, k and v must have the same shape (B, H, T, D)"),
-    ("T", 4194305, _lib.FPA_ERR_UNSUPPORTED, "T must be at most 4194304"),
+    ("T", 8388609, _lib.FPA_ERR_UNSUPPORTED, "T must be at most 8388608"),
     ("B", 65536, _lib.FPA_ERR_UNSUPPORTED, "B and H must each be at most 65535"),
     ("H", 65536, _lib.FPA_ERR_UNSUPPORTED, "B and H must each be at most 65535"),
 ])
@@ -132,9 +132,9 @@ def test_c_abi_validation(field, value, code, msg):
     assert msg in L.fpa_last_error().decode()
 
 
-@pytest.mark.parametrize("B,H,T,D", [(1, 1, 4194304, 64), (65535, 2, 64, 16), (1, 1, 64, 256)])
+@pytest.mark.parametrize("B,H,T,D", [(1, 1, 8388608, 64), (65535, 2, 64, 16), (1, 1, 64, 256)])
 def test_c_abi_accepts_the_envelope(B, H, T, D):
-    """Shapes at the edges of what the kernels take (T = 2^22, B * H > 65535, D = 256) pass
+    """Shapes at the edges of what the kernels take (T = 2^23, B * H > 65535, D = 256) pass
     validation: with NULL tensors the first complaint is about q, after every shape check."""
     L = _lib.lib()
     for dtype in (0, 1):

@@ -78,10 +78,10 @@ def _row_reference(q, k, v, phi, psi, beta, t):
     return p @ vd[: t + 1]
 
 
-@pytest.mark.parametrize("T", [131269, 1048641, 4194304])
+@pytest.mark.parametrize("T", [131269, 1048641, 8388608])
 def test_length_beyond_131072(fpa, T):
     """T = 131269 (2052 blocks of 64), T = 1048641 (16386 blocks: past the LDS staging of the mid pass)
-    and T = 4194304 (65536 blocks, the largest the library takes: 16 GiB of block-pair sums), one head,
+    and T = 8388608 (131072 blocks, the largest the library takes: 64 GiB of block-pair sums), one head,
     fp16 D16.
 
     With dO zero on every row >= T0 = 320, each output and gradient of positions < T0 equals that
