@@ -4,8 +4,9 @@
 //
 // Reference behaviour: kernel.py:103-162 (_fwd) of yliu-fort/first-passage-attention.
 // gfx950 design: a workgroup of FPA_NW waves owns 32 query rows per wave, streams 64-key tiles
-// from the diagonal down to key 0 through double-buffered (single-buffered for fp32 at D = 256,
-// where two stages do not fit in LDS), padded LDS tiles filled by direct global->LDS loads (one
+// from the diagonal down to key 0 through double-buffered (single-buffered for fp32 at D = 128 and 256,
+// where two stages of the workgroups that share a CU do not fit in LDS), padded LDS tiles filled by
+// direct global->LDS loads (one
 // barrier per tile), computes S^T = K Q^T and O^T += V^T P^T on the 32x32 MFMA (V^T read from the
 // row-major tile with LDS transpose reads), and keeps each query's online-softmax state in its own
 // lane.
@@ -68,7 +69,8 @@ fpa_fwd_kernel(FwdParams p) {
     constexpr int DT = D < 32 ? 32 : D;
     constexpr int NDT = DT / 32;
     constexpr int TB = Pad<T, DT>::template bytes<BN>();  // one padded K or V tile
-    constexpr int NS = tile_stages<TB>(2 * 4 * BN * 4);
+    // Two stages when WPE workgroups' worth of them (K, V and the per-key values) fit a CU's 160 KB.
+    constexpr int NS = (WPE * (4 * TB + 2 * 4 * BN * 4) <= 160 * 1024) ? 2 : 1;
     __shared__ __attribute__((aligned(1024))) char Ks[NS][TB];
     __shared__ __attribute__((aligned(1024))) char Vs[NS][TB];
     // Per-key values of a tile: CA, CP (SUF, PSI for fp32), PHI and BST (the block's BMIN at [3][0]).
@@ -358,8 +360,15 @@ __global__ void __launch_bounds__(256) fpa_fwd_merge_kernel(FwdParams p) {
     }
 }
 
+// Waves per SIMD of the forward.  At D = 128 two fit: fp16 in 236 VGPRs with no spills and two LDS
+// stages of K and V (70 KB per workgroup), fp32 in 256 with one register spilled outside the tile loop
+// and one stage (67 KB).  Against one wave per SIMD, whose 512-register budget the compiler had filled
+// (332 and 352 VGPRs): fp16 121 -> 85 us and fp32 531 -> 461 us at B4 H12 T2048, fp32 629 -> 593 us
+// at B2 H8 T4096.
 template <typename T, int D>
-constexpr int fwd_wpe() { return (D >= 128) ? 1 : (sizeof(T) == 2 ? FPA_FWD_WPE : FPA_FWD_WPE32); }
+constexpr int fwd_wpe() {
+    return (D == 128) ? 2 : (D >= 128) ? 1 : (sizeof(T) == 2 ? FPA_FWD_WPE : FPA_FWD_WPE32);
+}
 
 template <typename T, int D>
 static hipError_t launch_fwd_t(const FwdParams &p, hipStream_t s) {

@@ -26,7 +26,7 @@ WPE16, WPE32 = 3, 2                  # FPA_FWD_WPE, FPA_FWD_WPE32
 
 
 def wpe(dtype, D):
-    return 1 if D >= 128 else (WPE16 if dtype == 0 else WPE32)
+    return 2 if D == 128 else 1 if D > 128 else (WPE16 if dtype == 0 else WPE32)
 
 
 def split_tiles(BH, T, dtype, D):
@@ -123,6 +123,6 @@ def test_split_only_where_the_launch_is_short():
     assert split_tiles(32, 2048, 0, 64) == 8        # B2 H16: 512 workgroups
     assert split_tiles(36, 2048, 0, 64) == 0        # B3 H12: 576 workgroups
     assert split_tiles(48, 2048, 0, 64) == 0        # cfg2: 768 workgroups
-    assert split_tiles(16, 4096, 1, 128) == 0       # cfg3: 512 workgroups, 256 slots
+    assert split_tiles(16, 4096, 1, 128) == 0       # cfg3: 512 workgroups, 512 slots
     assert split_tiles(12, 16381, 0, 64) == 0       # cfg4
     assert split_tiles(2, 384, 0, 64) == 0          # three row tiles
