@@ -14,9 +14,9 @@
 #include "fpa_common.h"
 #include "fpa_params.h"
 
-// Tuning knobs (build-time): waves per SIMD of the D <= 64 forward kernel, fp16 and fp32.  Three
-// fp16 waves fit in 168 VGPRs each; with 3 workgroups per CU the cfg2 grid (768 workgroups) is
-// resident at once.  The fp32 D = 64 kernel needs about 200 VGPRs.
+// Tuning knobs (build-time): waves per SIMD of the D <= 64 forward kernel, fp16 and fp32 (fp32 at D <= 32
+// runs three: fwd_wpe).  Three fp16 waves fit in 168 VGPRs each; with 3 workgroups per CU the cfg2 grid
+// (768 workgroups) is resident at once.  The fp32 D = 64 kernel needs about 180 VGPRs.
 #ifndef FPA_FWD_WPE
 #define FPA_FWD_WPE 3
 #endif
@@ -364,10 +364,11 @@ __global__ void __launch_bounds__(256) fpa_fwd_merge_kernel(FwdParams p) {
 // stages of K and V (70 KB per workgroup), fp32 in 256 with one register spilled outside the tile loop
 // and one stage (67 KB).  Against one wave per SIMD, whose 512-register budget the compiler had filled
 // (332 and 352 VGPRs): fp16 121 -> 85 us and fp32 531 -> 461 us at B4 H12 T2048, fp32 629 -> 593 us
-// at B2 H8 T4096.
+// at B2 H8 T4096.  fp32 at D <= 32 fits three (141 and 152 VGPRs, no spills): 6-7% faster than two at
+// B4 H12 T2048 and B2 H8 T4096.
 template <typename T, int D>
 constexpr int fwd_wpe() {
-    return (D == 128) ? 2 : (D >= 128) ? 1 : (sizeof(T) == 2 ? FPA_FWD_WPE : FPA_FWD_WPE32);
+    return (D == 128) ? 2 : (D >= 128) ? 1 : (sizeof(T) == 2 ? FPA_FWD_WPE : (D <= 32 ? 3 : FPA_FWD_WPE32));
 }
 
 template <typename T, int D>

@@ -82,7 +82,7 @@ hipError_t launch_stats(const StatsParams &p, hipStream_t s) {
 
 int fwd_split_tiles(int64_t BH, int64_t T, int dtype, int D) {
     const int64_t nqt = (T + 32 * FPA_NW - 1) / (32 * FPA_NW);
-    const int wpe = (D == 128) ? 2 : (D >= 128) ? 1 : (dtype == 0 ? FPA_FWD_WPE : FPA_FWD_WPE32);  // fwd_wpe
+    const int wpe = (D == 128) ? 2 : (D >= 128) ? 1 : (dtype == 0 ? FPA_FWD_WPE : (D <= 32 ? 3 : FPA_FWD_WPE32));  // fwd_wpe
     if (nqt < 4 || 100 * BH * nqt > (int64_t)FPA_FWD_SPLIT_FILL * 8 * XCD_CUS * wpe) return 0;
     return (int)(nqt / 2);
 }

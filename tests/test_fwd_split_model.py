@@ -26,7 +26,7 @@ WPE16, WPE32 = 3, 2                  # FPA_FWD_WPE, FPA_FWD_WPE32
 
 
 def wpe(dtype, D):
-    return 2 if D == 128 else 1 if D > 128 else (WPE16 if dtype == 0 else WPE32)
+    return 2 if D == 128 else 1 if D > 128 else (WPE16 if dtype == 0 else (3 if D <= 32 else WPE32))
 
 
 def split_tiles(BH, T, dtype, D):
