@@ -196,6 +196,7 @@ SPLIT_CASES = [  # (B, H, T, D, dtype, beta, seed): shapes whose forward splits 
     (1, 2, 700, 64, torch.float16, None, 45),
     (1, 1, 513, 16, torch.float16, None, 46),      # fp16 D16: two 16-byte chunks per row in the merge
     (2, 4, 1000, 64, torch.float16, None, 47),     # B*H = 8: heads pinned to XCDs, items per XCD
+    (1, 2, 1100, 128, torch.float32, None, 48),    # fp32 D128: K, V single-buffered (two workgroups per CU)
 ]
 
 
